@@ -1,0 +1,113 @@
+"""AB-Attention and explicit sampling-plan reuse (MI355X build).
+
+Same public surface as the reference's ``ab_attention/attention.py``:
+``SamplePlan``, ``build_plan``, ``apply_plan`` and ``ab_attention`` with the
+same arguments, defaults, validation (ValueError) and plan layout.
+
+Differences that do not change results:
+  - the IBCS scratch budget per head chunk is sized for 288 GB of HBM, so the
+    Wan2.1-14B 720p call runs as one chunk instead of nine; rows are
+    independent and the offsets are drawn before chunking, so the plan does
+    not depend on the chunking (attention.py:54-75 in the reference);
+  - ``apply_plan`` goes to the gfx950 paged prefill in ``paged.py``.
+"""
+import math
+from typing import NamedTuple
+
+import torch
+
+# IBCS keeps [rows, 8, ~tokens/4] fp16 pair-LSEs per head chunk.
+_LSE_BUDGET_BYTES = 16 * 1024 * 1024 * 1024
+
+
+class SamplePlan(NamedTuple):
+    """SIP sample and log2(1/pi) weights, shaped [rows, pages, 32].
+
+    ``descriptor``  - int32, sampled KV4 block ids, shape [rows, pages, 32].
+    ``log_weights`` - float32, log2 inverse-inclusion weights, same shape.
+
+    ``rows`` is batch * heads * ceil_div(tokens, 128); ``pages`` is
+    ``sample_pages``; each page packs 32 sampled KV4 blocks. Ids are local to
+    their head. Treat both tensors as read-only; build a new plan to refresh
+    the selection. (Reference: attention.py:11-23.)
+    """
+
+    descriptor: torch.Tensor
+    log_weights: torch.Tensor
+
+
+def _heads_per_chunk(batch_heads: int, q_blocks: int, tokens: int) -> int:
+    lse_bytes_per_head = q_blocks * 8 * (tokens // 4) * 2
+    return max(1, min(batch_heads, _LSE_BUDGET_BYTES // lse_bytes_per_head))
+
+
+@torch.no_grad()
+def build_plan(q, k, *, sample_pages=64, seed=42):
+    """Score and sample ``sample_pages * 128`` keys per 128-query block.
+
+    Q and K must have shape [batch, heads, tokens, 128], bf16, on the same
+    GPU; tokens must be divisible by 4 and exceed the sampled key count.
+    IBCS scores KV4 blocks through 8 query-cluster centroids and pooled key
+    pairs; SIP draws ``sample_pages * 32`` blocks without replacement and
+    returns log2(1/pi) weights used as logit shifts at attention time.
+    Returns a ``SamplePlan`` with both tensors shaped [rows, pages, 32].
+    (Reference: attention.py:26-82.)
+    """
+    sample_pages = int(sample_pages)
+    if q.ndim != 4 or q.shape != k.shape or q.shape[2] % 4:
+        raise ValueError("Q/K must match [B,H,N,D] with N divisible by 4")
+    if sample_pages <= 0:
+        raise ValueError("sample_pages must be positive")
+    if sample_pages * 128 >= q.shape[2]:
+        raise ValueError("sampled key count must be smaller than the sequence length")
+    from . import _C as ops
+
+    batch_heads = q.shape[0] * q.shape[1]
+    tokens, dim = q.shape[2:]
+    q_blocks = math.ceil(tokens / 128)
+    rows, samples = batch_heads * q_blocks, sample_pages * 32
+
+    # All offsets are drawn before chunking, so chunking cannot change the plan.
+    generator = torch.Generator(device=q.device).manual_seed(seed)
+    offsets = torch.rand(rows, device=q.device, generator=generator)
+    flat_q = q.reshape(batch_heads, tokens, dim)
+    flat_k = k.reshape(batch_heads, tokens, dim)
+
+    heads_per_chunk = _heads_per_chunk(batch_heads, q_blocks, tokens)
+    sampled = torch.empty((rows, samples), dtype=torch.int32, device=q.device)
+    log_weights = torch.empty((rows, samples), dtype=torch.float32, device=q.device)
+
+    for start in range(0, batch_heads, heads_per_chunk):
+        stop = min(batch_heads, start + heads_per_chunk)
+        first, last = start * q_blocks, stop * q_blocks
+        scores = ops.ibcs(
+            flat_q[start:stop].unsqueeze(0).contiguous(),
+            flat_k[start:stop].unsqueeze(0).contiguous(),
+        )
+        ops.sip(scores, offsets[first:last], sampled[first:last], log_weights[first:last])
+        del scores
+
+    return SamplePlan(
+        sampled.reshape(rows, sample_pages, 32),
+        log_weights.reshape(rows, sample_pages, 32),
+    )
+
+
+@torch.no_grad()
+def apply_plan(q, k, v, plan, *, return_lse=False):
+    """Weighted sparse attention of q over each row's sampled KV4 blocks.
+
+    A plan can be reused across denoising steps while the tensor shape and
+    device stay the same. With ``return_lse`` the base-2 softmax normaliser is
+    also returned as float32 [batch, heads, tokens], for merging attention
+    partitions. (Reference: attention.py:85-96.)
+    """
+    from .paged import paged_attention
+
+    return paged_attention(q, k, v, *plan, return_lse=return_lse)
+
+
+@torch.no_grad()
+def ab_attention(q, k, v, *, sample_pages=64, seed=42):
+    """AB-Attention with a fresh sampling plan; output has Q's shape and dtype."""
+    return apply_plan(q, k, v, build_plan(q, k, sample_pages=sample_pages, seed=seed))

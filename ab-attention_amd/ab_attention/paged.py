@@ -1,0 +1,75 @@
+"""Weighted paged sparse prefill on gfx950.
+
+``paged_attention`` keeps the reference's signature, validation (ValueError)
+and output/LSE layout (ab_attention/flashinfer_backend.py:164-242). The
+arithmetic is ``ab_paged_prefill`` in libab_attention_hip.so: a bf16 MFMA
+flash-attention kernel that reads each row's KV4 blocks straight from K/V by
+their per-head ids and adds the SIP weight of each block to its logits
+(the reference's ABSipAttention variant, flashinfer_backend.py:30-59).
+
+The reference translates per-head ids into a global page table and caches it
+per descriptor (flashinfer_backend.py:62-74, :202-217); the kernel here
+indexes K/V by (head, id) directly, so there is no table and no cache to keep
+coherent. Queries are not padded either: the tail of the last query block is
+simply not stored (the reference computes it on zero-padded queries and drops
+it, flashinfer_backend.py:77-91, :236-242).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+
+_HEAD_DIM = 128
+_QUERY_BLOCK = 128
+_PAGE_SIZE = 4
+
+
+@torch.no_grad()
+def paged_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    descriptor: torch.Tensor,
+    log_weights: torch.Tensor,
+    *,
+    return_lse: bool = False,
+):
+    """Weighted sparse attention over the plan's KV4 blocks; returns o (and base-2 lse)."""
+    if q.ndim != 4 or q.shape != k.shape or q.shape != v.shape:
+        raise ValueError("Q/K/V must have the same [B,H,N,D] shape")
+    if q.device != k.device or q.device != v.device:
+        raise ValueError("Q/K/V must be on the same CUDA device")
+    if q.device.type != "cuda":
+        raise ValueError("paged attention requires GPU tensors")
+    if q.dtype != torch.bfloat16 or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("paged attention requires BF16 Q/K/V")
+    if q.shape[-1] != _HEAD_DIM or q.shape[2] % _PAGE_SIZE:
+        raise ValueError("paged attention requires head_dim=128 and N divisible by 4")
+    batch, heads, tokens, dim = q.shape
+    batch_heads = batch * heads
+    rows = batch_heads * math.ceil(tokens / _QUERY_BLOCK)
+    if (descriptor.ndim != 3 or descriptor.shape != log_weights.shape
+            or descriptor.shape[0] != rows or descriptor.shape[-1] != 32):
+        raise ValueError(f"descriptor and log_weights must share [{rows}, pages, 32] shape")
+    if descriptor.device != q.device or log_weights.device != q.device:
+        raise ValueError("descriptor and log_weights must be on the Q device")
+
+    samples = descriptor.shape[1] * 32
+    q = q.contiguous()
+    k = k.contiguous()
+    v = v.contiguous()
+    ids = descriptor.to(torch.int32).contiguous()
+    weights = log_weights.to(torch.float32).contiguous()
+    output = torch.empty_like(q)
+    lse = torch.empty((batch, heads, tokens), dtype=torch.float32, device=q.device) if return_lse else None
+    lib = _lib.load()
+    with torch.cuda.device(q.device):
+        _lib.check(lib.ab_paged_prefill(
+            _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), batch_heads, tokens, _lib.ptr(ids),
+            _lib.ptr(weights), samples, _lib.ptr(output), _lib.ptr(lse), _lib.stream(q.device)))
+    if not return_lse:
+        return output
+    return output, lse

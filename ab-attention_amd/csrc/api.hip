@@ -1,0 +1,198 @@
+// C-ABI of the gfx950 AB-Attention library (declared in include/ab_attention.h).
+//
+// Every entry point validates its sizes before any launch, enqueues on the
+// caller's stream, never synchronises and never allocates: buffers, including
+// workspace, belong to the caller. Failures return a nonzero status and leave
+// a message for ab_last_error().
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+
+#include "../../include/ab_attention.h"
+#include "common.hpp"
+
+namespace ab {
+
+int64_t lse_stride(int64_t fb);
+int launch_cluster_pool(const void* q, const void* k, int64_t bh, int64_t n, void* centroids, float* pops,
+                        void* pooled, float qk_scale_log2, hipStream_t stream);
+int launch_lse(const void* centroids, const void* pooled, int64_t bh, int64_t n, void* lse, float* lse_max,
+               float* lse_den, hipStream_t stream);
+int launch_masses(const void* lse, const float* pops, const float* lse_max, const float* lse_den, int64_t rows,
+                  int64_t fb, float* scores, hipStream_t stream);
+int launch_sip(const float* scores, const float* offsets, int64_t rows, int64_t population, int64_t samples,
+               int32_t* ids, float* logw, hipStream_t stream);
+bool sip_fits(int64_t population);
+int launch_prefill(const void* q, const void* k, const void* v, int64_t bh, int64_t n, const int32_t* ids,
+                   const float* logw, int64_t samples, void* out, float* lse, hipStream_t stream);
+
+namespace {
+thread_local char g_error[512] = "";
+
+// float(128^-0.5 * log2(e)) as computed by the reference host code
+// (csrc/ibcs.cu:601-602).
+float qk_scale_log2() { return static_cast<float>(std::pow(128.0, -0.5) * 1.4426950408889634); }
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+struct IbcsLayout {
+    int64_t qb, fb, rows, ld;
+    size_t centroids, pops, pooled, lse, lse_max, lse_den, total;
+};
+
+IbcsLayout ibcs_layout(int64_t bh, int64_t n) {
+    IbcsLayout L;
+    L.qb = (n + kQueryBlock - 1) / kQueryBlock;
+    L.fb = n / kKvBlock;
+    L.rows = bh * L.qb;
+    L.ld = lse_stride(L.fb);
+    size_t off = 0;
+    L.centroids = off;
+    off = align256(off + size_t(L.rows) * kCentroids * kHeadDim * 2);
+    L.pops = off;
+    off = align256(off + size_t(L.rows) * kCentroids * 4);
+    L.pooled = off;
+    off = align256(off + size_t(bh) * L.fb * kReps * kHeadDim * 2);
+    L.lse = off;
+    off = align256(off + size_t(L.rows) * kCentroids * L.ld * 2);
+    L.lse_max = off;
+    off = align256(off + size_t(L.rows) * kCentroids * 4);
+    L.lse_den = off;
+    off = align256(off + size_t(L.rows) * kCentroids * 4);
+    L.total = off;
+    return L;
+}
+
+int check_qk_shape(const char* what, int64_t bh, int64_t n) {
+    if (bh <= 0 || n <= 0) return set_error(AB_ERR_INVALID, "%s: batch_heads and tokens must be positive", what);
+    if (n % kKvBlock) return set_error(AB_ERR_INVALID, "%s: sequence length must be divisible by 4", what);
+    if (n / kKvBlock > kMaxKvBlocks)
+        return set_error(AB_ERR_INVALID, "%s: KV4 block count must be in [1, 32768]", what);
+    const int64_t qb = (n + kQueryBlock - 1) / kQueryBlock;
+    if (qb > 65535 || bh > 65535) return set_error(AB_ERR_INVALID, "%s: grid too large", what);
+    return AB_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+}  // namespace
+
+int set_error(int code, const char* fmt, ...) {
+    va_list args;
+    va_start(args, fmt);
+    vsnprintf(g_error, sizeof(g_error), fmt, args);
+    va_end(args);
+    return code;
+}
+
+int check_launch(const char* what) {
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return set_error(AB_ERR_LAUNCH, "%s launch failed: %s", what, hipGetErrorString(err));
+    return AB_OK;
+}
+
+}  // namespace ab
+
+using namespace ab;
+
+extern "C" {
+
+const char* ab_last_error(void) { return g_error; }
+
+int ab_abi_version(void) { return AB_ABI_VERSION; }
+
+int64_t ab_ibcs_lse_stride(int64_t tokens) { return lse_stride(tokens / kKvBlock); }
+
+size_t ab_ibcs_workspace_bytes(int64_t batch_heads, int64_t tokens) {
+    if (batch_heads <= 0 || tokens <= 0) return 0;
+    return ibcs_layout(batch_heads, tokens).total;
+}
+
+int ab_ibcs_cluster_pool(const void* q, const void* k, int64_t batch_heads, int64_t tokens, void* centroids,
+                         float* populations, void* pooled_keys, void* stream) {
+    if (int rc = check_qk_shape("ibcs", batch_heads, tokens)) return rc;
+    if (!q || !k || !centroids || !populations || !pooled_keys)
+        return set_error(AB_ERR_INVALID, "ibcs: null pointer");
+    if (!aligned16(q) || !aligned16(k) || !aligned16(pooled_keys))
+        return set_error(AB_ERR_INVALID, "ibcs: q, k and pooled keys must be 16-byte aligned");
+    return launch_cluster_pool(q, k, batch_heads, tokens, centroids, populations, pooled_keys, qk_scale_log2(),
+                               static_cast<hipStream_t>(stream));
+}
+
+int ab_ibcs_lse(const void* centroids, const void* pooled_keys, int64_t batch_heads, int64_t tokens,
+                void* block_lse, float* lse_max, float* lse_den, void* stream) {
+    if (int rc = check_qk_shape("ibcs", batch_heads, tokens)) return rc;
+    if (!centroids || !pooled_keys || !block_lse || !lse_max || !lse_den)
+        return set_error(AB_ERR_INVALID, "ibcs: null pointer");
+    if (!aligned16(centroids) || !aligned16(pooled_keys) || !aligned16(block_lse))
+        return set_error(AB_ERR_INVALID, "ibcs: centroids, pooled keys and block LSE must be 16-byte aligned");
+    return launch_lse(centroids, pooled_keys, batch_heads, tokens, block_lse, lse_max, lse_den,
+                      static_cast<hipStream_t>(stream));
+}
+
+int ab_ibcs_masses(const void* block_lse, const float* populations, const float* lse_max, const float* lse_den,
+                   int64_t rows, int64_t kv_blocks, float* scores, void* stream) {
+    if (rows < 0 || kv_blocks <= 0 || kv_blocks > kMaxKvBlocks)
+        return set_error(AB_ERR_INVALID, "ibcs: bad masses shape");
+    if (!block_lse || !populations || !lse_max || !lse_den || !scores)
+        return set_error(AB_ERR_INVALID, "ibcs: null pointer");
+    if (!aligned16(block_lse)) return set_error(AB_ERR_INVALID, "ibcs: block LSE must be 16-byte aligned");
+    if (rows == 0) return AB_OK;
+    return launch_masses(block_lse, populations, lse_max, lse_den, rows, kv_blocks, scores,
+                         static_cast<hipStream_t>(stream));
+}
+
+int ab_ibcs(const void* q, const void* k, int64_t batch_heads, int64_t tokens, void* workspace,
+            size_t workspace_bytes, float* scores, void* stream) {
+    if (int rc = check_qk_shape("ibcs", batch_heads, tokens)) return rc;
+    if (!q || !k || !workspace || !scores) return set_error(AB_ERR_INVALID, "ibcs: null pointer");
+    const IbcsLayout L = ibcs_layout(batch_heads, tokens);
+    if (workspace_bytes < L.total)
+        return set_error(AB_ERR_INVALID, "ibcs: workspace of %zu bytes is smaller than the %zu required",
+                         workspace_bytes, L.total);
+    if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+        return set_error(AB_ERR_INVALID, "ibcs: workspace must be 256-byte aligned");
+    char* ws = static_cast<char*>(workspace);
+    if (int rc = ab_ibcs_cluster_pool(q, k, batch_heads, tokens, ws + L.centroids,
+                                      reinterpret_cast<float*>(ws + L.pops), ws + L.pooled, stream))
+        return rc;
+    if (int rc = ab_ibcs_lse(ws + L.centroids, ws + L.pooled, batch_heads, tokens, ws + L.lse,
+                             reinterpret_cast<float*>(ws + L.lse_max), reinterpret_cast<float*>(ws + L.lse_den),
+                             stream))
+        return rc;
+    return ab_ibcs_masses(ws + L.lse, reinterpret_cast<const float*>(ws + L.pops),
+                          reinterpret_cast<const float*>(ws + L.lse_max),
+                          reinterpret_cast<const float*>(ws + L.lse_den), L.rows, L.fb, scores, stream);
+}
+
+int ab_sip(const float* scores, const float* offsets, int64_t rows, int64_t population, int64_t samples,
+           int32_t* ids, float* log_weights, void* stream) {
+    if (rows < 0) return set_error(AB_ERR_INVALID, "sip: negative row count");
+    if (!(samples > 0 && samples < population))
+        return set_error(AB_ERR_INVALID, "sip: sample count must be inside the population");
+    if (population > (int64_t(1) << 30)) return set_error(AB_ERR_INVALID, "sip: population too large");
+    if (!sip_fits(population))
+        return set_error(AB_ERR_INVALID, "sip: population exceeds single-workgroup LDS capacity");
+    if (rows > 0 && (!scores || !offsets || !ids || !log_weights))
+        return set_error(AB_ERR_INVALID, "sip: null pointer");
+    if (rows > 0xffffffffll) return set_error(AB_ERR_INVALID, "sip: too many rows");
+    return launch_sip(scores, offsets, rows, population, samples, ids, log_weights,
+                      static_cast<hipStream_t>(stream));
+}
+
+int ab_paged_prefill(const void* q, const void* k, const void* v, int64_t batch_heads, int64_t tokens,
+                     const int32_t* ids, const float* log_weights, int64_t samples, void* out, float* lse,
+                     void* stream) {
+    if (int rc = check_qk_shape("paged_prefill", batch_heads, tokens)) return rc;
+    if (samples <= 0 || samples % kBlocksPerPage)
+        return set_error(AB_ERR_INVALID, "paged_prefill: samples must be a positive multiple of 32");
+    if (!q || !k || !v || !ids || !log_weights || !out)
+        return set_error(AB_ERR_INVALID, "paged_prefill: null pointer");
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || (reinterpret_cast<uintptr_t>(out) & 7u))
+        return set_error(AB_ERR_INVALID, "paged_prefill: q/k/v must be 16-byte and out 8-byte aligned");
+    const int64_t rows = batch_heads * ((tokens + kQueryBlock - 1) / kQueryBlock);
+    if (rows * 8 > 0xffffffffll) return set_error(AB_ERR_INVALID, "paged_prefill: too many rows");
+    return launch_prefill(q, k, v, batch_heads, tokens, ids, log_weights, samples, out, lse,
+                          static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

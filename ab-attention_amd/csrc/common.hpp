@@ -1,0 +1,58 @@
+// Shared definitions for the gfx950 AB-Attention kernels.
+//
+// Geometry is fixed by the reference (csrc/ibcs.cu:32-36,
+// ab_attention/flashinfer_backend.py:19-21): head dim 128, 128-query blocks,
+// 4-key (KV4) blocks, 8 centroids per query block, 2 key representatives per
+// KV4 block, 32 KV4 blocks per sample page.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace ab {
+
+constexpr int kHeadDim = 128;
+constexpr int kQueryBlock = 128;
+constexpr int kKvBlock = 4;
+constexpr int kCentroids = 8;
+constexpr int kReps = 2;
+constexpr int kBlocksPerPage = 32;
+constexpr int64_t kMaxKvBlocks = 32768;  // csrc/ibcs.cu:567-568
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf16_lo(uint32_t packed) { return __uint_as_float(packed << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t packed) { return __uint_as_float(packed & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t bits) { return __uint_as_float(uint32_t(bits) << 16); }
+
+// Round-to-nearest-even float -> bfloat16 bits (NaN kept quiet).
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+    return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+}
+
+// Hardware base-2 exponential and logarithm (v_exp_f32 / v_log_f32).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+__device__ __forceinline__ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace ab
+
+// Error reporting shared by every C-ABI entry point (api.hip).
+namespace ab {
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+}  // namespace ab

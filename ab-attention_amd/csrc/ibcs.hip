@@ -1,0 +1,481 @@
+// IBCS on gfx950: query clustering + key pooling, centroid/key pair-LSE with
+// per-centroid normalisers, and population-weighted block masses.
+//
+// Dataflow (one head chunk, the caller's workspace holds every intermediate):
+//   cluster_pool_kernel  Q,K -> scaled centroids [rows,8,128] bf16, populations
+//                        [rows,8] f32, pooled keys [bh,fb,2,128] bf16
+//   lse_kernel           centroids x pooled keys (bf16 MFMA) -> fp16 pair-LSE
+//                        [rows,8,ld] and (max, den) [rows,8]
+//   masses_kernel        pair-LSE + normalisers + populations -> scores [rows,fb]
+//
+// Reference stages: csrc/ibcs.cu:106-238 (cluster), :244-266 (pool),
+// :329-489 (LSE), :495-538 (scores). Exactness notes:
+//   - cluster/pool follow the reference's fp32 operation order (lane-strided
+//     fmaf chains, xor-butterfly sums, row-order centroid sums, IEEE division),
+//     so they match the CPU oracle bit for bit;
+//   - pair-LSE uses one exp2 and one log2 per (centroid, block):
+//     exp2(a-mx) + exp2(b-mx) == 1 + exp2(min-mx) because exp2(0) == 1. The
+//     reference's max(sum, 1e-20) floor never binds for finite inputs (sum >= 1);
+//   - the normaliser D is accumulated tile by tile from the fp16-rounded values
+//     (online max/rescale), matching the reference up to fp32 rounding order.
+#include <cfloat>
+
+#include "common.hpp"
+
+namespace ab {
+namespace {
+
+// ---------------------------------------------------------------------------
+// Stage 1+2: clustering of one 128-query block and pooling of the same 128
+// key tokens. One workgroup of 128 threads per (query block, head): thread i
+// owns query i (kept in 128 VGPRs); thread d owns dim d for the column sums.
+
+constexpr int kClusterThreads = 128;
+constexpr int kRowWords = kHeadDim / 2 + 1;  // padded bf16 row: 65 dwords
+
+// Squared distance with the reference association (csrc/ibcs.cu:143-155,
+// :171-181): partial l chains fmaf over dims l, l+32, l+64, l+96; the 32
+// partials are summed by the xor butterfly 16,8,4,2,1 (every lane of a
+// butterfly ends with the pairwise tree below).
+__device__ __forceinline__ float lane_distance(const float (&x)[kHeadDim],
+                                               const float* __restrict__ center) {
+    float p[32];
+#pragma unroll
+    for (int l = 0; l < 32; ++l) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float delta = x[l + 32 * r] - center[l + 32 * r];
+            acc = __builtin_fmaf(delta, delta, acc);
+        }
+        p[l] = acc;
+    }
+#pragma unroll
+    for (int mask = 16; mask >= 1; mask >>= 1)
+#pragma unroll
+        for (int l = 0; l < mask; ++l) p[l] = p[l] + p[l + mask];
+    return p[0];
+}
+
+// Block-wide argmax over 128 threads: largest value, lowest index on ties
+// (cub::ArgMax semantics, csrc/ibcs.cu:94-102). Result valid in every thread.
+__device__ __forceinline__ int block_argmax(float value, int index, float* s_val, int* s_idx) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(value, off);
+        const int oi = __shfl_xor(index, off);
+        if (ov > value || (ov == value && oi < index)) {
+            value = ov;
+            index = oi;
+        }
+    }
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        s_val[wave] = value;
+        s_idx[wave] = index;
+    }
+    __syncthreads();
+    const float v0 = s_val[0], v1 = s_val[1];
+    const int i0 = s_idx[0], i1 = s_idx[1];
+    __syncthreads();
+    return (v1 > v0 || (v1 == v0 && i1 < i0)) ? i1 : i0;
+}
+
+__device__ __forceinline__ float block_elem(const uint32_t* block, int row, int dim) {
+    const uint32_t w = block[row * kRowWords + (dim >> 1)];
+    return (dim & 1) ? bf16_hi(w) : bf16_lo(w);
+}
+
+__global__ __launch_bounds__(kClusterThreads) void cluster_pool_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    uint16_t* __restrict__ centroids, float* __restrict__ pops, uint16_t* __restrict__ pooled,
+    int64_t n, int64_t qb, float qk_scale_log2) {
+    __shared__ uint32_t block[kQueryBlock * kRowWords];
+    __shared__ float center_row[kHeadDim];
+    __shared__ float s_val[2];
+    __shared__ int s_idx[2];
+    __shared__ int assignment[kQueryBlock];
+    __shared__ int members[kQueryBlock];
+    __shared__ int counts[kCentroids];
+    __shared__ int starts[kCentroids];
+
+    const int tid = threadIdx.x;
+    const int64_t blk = blockIdx.x, bh = blockIdx.y;
+    const int64_t base = blk * kQueryBlock;
+    const int valid = static_cast<int>(min<int64_t>(kQueryBlock, n - base));
+    const int64_t row = bh * qb + blk;
+
+    // Stage the query block (zero rows past the sequence end).
+    const u32x4* src = reinterpret_cast<const u32x4*>(q + (bh * n + base) * kHeadDim);
+    for (int idx = tid; idx < kQueryBlock * 16; idx += kClusterThreads) {
+        const int r = idx >> 4, c = idx & 15;
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (r < valid) v = src[idx];
+        uint32_t* dst = block + r * kRowWords + c * 4;
+        dst[0] = v.x;
+        dst[1] = v.y;
+        dst[2] = v.z;
+        dst[3] = v.w;
+    }
+    __syncthreads();
+
+    // Per-dim mean over valid queries in row order (csrc/ibcs.cu:130-140).
+    {
+        float sum = 0.0f;
+        for (int i = 0; i < valid; ++i) sum += block_elem(block, i, tid);
+        center_row[tid] = __fdiv_rn(sum, static_cast<float>(valid));
+    }
+    float x[kHeadDim];
+#pragma unroll
+    for (int w = 0; w < kHeadDim / 2; ++w) {
+        const uint32_t v = block[tid * kRowWords + w];
+        x[2 * w] = bf16_lo(v);
+        x[2 * w + 1] = bf16_hi(v);
+    }
+    __syncthreads();
+
+    // Farthest-first centres with nearest-centre assignment (:158-197).
+    const bool live = tid < valid;
+    float min_d = live ? lane_distance(x, center_row) : -INFINITY;
+    int center = block_argmax(min_d, tid, s_val, s_idx);
+    min_d = INFINITY;
+    int assign = 0;
+    for (int slot = 0; slot < kCentroids; ++slot) {
+        center_row[tid] = block_elem(block, center, tid);
+        __syncthreads();
+        if (live) {
+            const float dist = lane_distance(x, center_row);
+            if (dist < min_d) {
+                min_d = dist;
+                assign = slot;
+            }
+        }
+        if (slot + 1 < kCentroids) center = block_argmax(live ? min_d : -INFINITY, tid, s_val, s_idx);
+        __syncthreads();
+    }
+
+    // Populations and a slot-major member list that keeps query order.
+    assignment[tid] = live ? assign : -1;
+    __syncthreads();
+    if (tid < kCentroids) {
+        int c = 0;
+        for (int i = 0; i < valid; ++i) c += assignment[i] == tid;
+        counts[tid] = c;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int s = 0;
+        for (int c = 0; c < kCentroids; ++c) {
+            starts[c] = s;
+            s += counts[c];
+        }
+    }
+    __syncthreads();
+    if (live) {
+        int rank = 0;
+        for (int i = 0; i < tid; ++i) rank += assignment[i] == assign;
+        members[starts[assign] + rank] = tid;
+    }
+    __syncthreads();
+    if (tid < kCentroids) pops[row * kCentroids + tid] = static_cast<float>(counts[tid]);
+
+    // Centroid = bf16(member sum / count), then the LSE pre-scale
+    // bf16(centroid * 128^-0.5 * log2 e) (csrc/ibcs.cu:213-237, :293-295).
+    {
+        uint16_t* dst = centroids + row * kCentroids * kHeadDim + tid;
+        for (int s = 0; s < kCentroids; ++s) {
+            const int cnt = counts[s], first = starts[s];
+            float sum = 0.0f;
+            for (int t = 0; t < cnt; ++t) sum += block_elem(block, members[first + t], tid);
+            const uint32_t c = cnt > 0 ? f32_to_bf16(__fdiv_rn(sum, static_cast<float>(cnt))) : 0u;
+            dst[s * kHeadDim] = static_cast<uint16_t>(f32_to_bf16(__uint_as_float(c << 16) * qk_scale_log2));
+        }
+    }
+
+    // Pool the same tokens' keys: bf16(0.5 * (k_2r + k_2r+1)) (:244-266).
+    const u32x4* ksrc = reinterpret_cast<const u32x4*>(k + (bh * n + base) * kHeadDim);
+    u32x4* kdst = reinterpret_cast<u32x4*>(pooled + (bh * (n / 2) + base / 2) * kHeadDim);
+    const int pairs = valid / 2;
+    for (int idx = tid; idx < pairs * 16; idx += kClusterThreads) {
+        const int p = idx >> 4, c = idx & 15;
+        const u32x4 a = ksrc[(2 * p) * 16 + c];
+        const u32x4 b = ksrc[(2 * p + 1) * 16 + c];
+        u32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float lo = 0.5f * (bf16_lo(a[e]) + bf16_lo(b[e]));
+            const float hi = 0.5f * (bf16_hi(a[e]) + bf16_hi(b[e]));
+            o[e] = pack_bf16(lo, hi);
+        }
+        kdst[p * 16 + c] = o;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Stage 3: pair-LSE of every (centroid, KV4 block) with online normalisers.
+//
+// One workgroup = 4 waves = 8 query blocks (64 centroid rows) of one head; it
+// streams all of the head's pooled keys through LDS in tiles of 64 KV4 blocks
+// (128 pooled rows, 32 KiB, double buffered). Each wave computes a 16 x 64
+// tile per rep with v_mfma_f32_16x16x32_bf16: A = its 16 centroid rows (kept
+// in registers), B = pooled rows. MFMA column c of n-tile nt is KV4 block
+// 4c + nt, so a lane holds 4 consecutive blocks per centroid row and stores
+// them as one 8-byte fp16 vector.
+
+constexpr int kLseThreads = 256;
+constexpr int kLseQBlocks = 8;            // query blocks per workgroup
+constexpr int kLseTileBlocks = 64;        // KV4 blocks per LDS tile
+constexpr int kLseTileRows = kLseTileBlocks * kReps;
+constexpr int kLseStageBytes = kLseTileRows * kHeadDim * 2;  // 32 KiB
+
+__device__ __forceinline__ int lse_swizzle(int row, int chunk) {
+    return row * 16 + (chunk ^ ((row >> 3) & 15));
+}
+
+__device__ __forceinline__ void combine_pair(float& m, float& d, float om, float od) {
+    const float nm = fmaxf(m, om);
+    d = d * fast_exp2(m - nm) + od * fast_exp2(om - nm);
+    m = nm;
+}
+
+__global__ __launch_bounds__(kLseThreads, 2) void lse_kernel(
+    const uint16_t* __restrict__ centroids, const uint16_t* __restrict__ pooled,
+    _Float16* __restrict__ lse, float* __restrict__ lse_max, float* __restrict__ lse_den,
+    int64_t qb, int fb, int64_t ld, int groups_per_head, int total_groups) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    auto stage = [&](int i) { return reinterpret_cast<u32x4*>(smem + i * kLseStageBytes); };
+
+    // XCD-aware order: hardware deals workgroups round-robin over 8 XCDs, so
+    // consecutive logical groups (same head) are given to one XCD.
+    const int hw = blockIdx.x;
+    const int per_xcd = (total_groups + 7) / 8;
+    const int logical = (hw & 7) * per_xcd + (hw >> 3);
+    if (logical >= total_groups) return;
+    const int64_t bh = logical / groups_per_head;
+    const int64_t qgroup = logical % groups_per_head;
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int col = lane & 15, quad = lane >> 4;
+
+    // A operand: centroid row (wave*16 + col), dims 32s + 8*quad .. +8.
+    const int64_t qblock0 = qgroup * kLseQBlocks + wave * 2;
+    bf16x8 a_op[4];
+    {
+        const int64_t qbk = qblock0 + (col >> 3);
+        const int cent = col & 7;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            u32x4 v = {0u, 0u, 0u, 0u};
+            if (qbk < qb)
+                v = *reinterpret_cast<const u32x4*>(
+                    centroids + ((bh * qb + qbk) * kCentroids + cent) * kHeadDim + 32 * s + 8 * quad);
+            a_op[s] = __builtin_bit_cast(bf16x8, v);
+        }
+    }
+
+    const u32x4* head_keys = reinterpret_cast<const u32x4*>(pooled + bh * int64_t(fb) * kReps * kHeadDim);
+    const int tiles = (fb + kLseTileBlocks - 1) / kLseTileBlocks;
+
+    auto load_tile = [&](int tile, u32x4 (&regs)[8]) {
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+            const int idx = p * kLseThreads + tid;  // 16-byte chunk within the tile
+            const int r = idx >> 4;
+            const int blockj = tile * kLseTileBlocks + (r >> 1);
+            u32x4 v = {0u, 0u, 0u, 0u};
+            if (blockj < fb) v = head_keys[int64_t(tile) * kLseTileRows * 16 + idx];
+            regs[p] = v;
+        }
+    };
+    auto store_tile = [&](u32x4* dst, const u32x4 (&regs)[8]) {
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+            const int idx = p * kLseThreads + tid;
+            dst[lse_swizzle(idx >> 4, idx & 15)] = regs[p];
+        }
+    };
+
+    // Output rows owned by this lane: centroid rows quad*4 + v of the wave.
+    const int64_t my_qblock = qblock0 + (quad >> 1);
+    const bool row_ok = my_qblock < qb;
+    const int cent0 = (quad & 1) * 4;
+    _Float16* out_row = lse + ((bh * qb + my_qblock) * kCentroids + cent0) * ld;
+
+    float run_max[4], run_den[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        run_max[v] = -FLT_MAX;
+        run_den[v] = 0.0f;
+    }
+
+    u32x4 regs[8];
+    load_tile(0, regs);
+    store_tile(stage(0), regs);
+    __syncthreads();
+
+    for (int tile = 0; tile < tiles; ++tile) {
+        const bool more = tile + 1 < tiles;
+        if (more) load_tile(tile + 1, regs);
+        const u32x4* cur = stage(tile & 1);
+
+        f32x4 acc[4][2];
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const int prow = 2 * (4 * col + nt) + r;
+                f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const bf16x8 b = __builtin_bit_cast(bf16x8, cur[lse_swizzle(prow, 4 * s + quad)]);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_op[s], b, c, 0, 0, 0);
+                }
+                acc[nt][r] = c;
+            }
+        }
+
+        // Epilogue: lane holds centroid rows quad*4+v, blocks 4*col + nt.
+        const int jbase = tile * kLseTileBlocks + 4 * col;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            float f[4];
+            _Float16 h[4];
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt) {
+                const float a = acc[nt][0][v] + 1.0f;
+                const float b = acc[nt][1][v] + 1.0f;
+                const float mx = fmaxf(a, b), mn = fminf(a, b);
+                const float l = mx + fast_log2(1.0f + fast_exp2(mn - mx));
+                h[nt] = static_cast<_Float16>(l);
+                f[nt] = (jbase + nt < fb) ? static_cast<float>(h[nt]) : -INFINITY;
+            }
+            if (row_ok && jbase < fb) {
+                typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+                const f16x4 packed = {h[0], h[1], h[2], h[3]};
+                *reinterpret_cast<f16x4*>(out_row + int64_t(v) * ld + jbase) = packed;
+            }
+            const float tmax = fmaxf(fmaxf(f[0], f[1]), fmaxf(f[2], f[3]));
+            const float nm = fmaxf(run_max[v], tmax);
+            float d = run_den[v] * fast_exp2(run_max[v] - nm);
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt) d += fast_exp2(f[nt] - nm);
+            run_den[v] = d;
+            run_max[v] = nm;
+        }
+
+        if (more) store_tile(stage((tile + 1) & 1), regs);
+        __syncthreads();
+    }
+
+    // Merge the 16 lanes (columns) that share each centroid row.
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const float om = __shfl_xor(run_max[v], off);
+            const float od = __shfl_xor(run_den[v], off);
+            combine_pair(run_max[v], run_den[v], om, od);
+        }
+    }
+    if (col == 0 && row_ok) {
+        const int64_t slot = (bh * qb + my_qblock) * kCentroids + cent0;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            lse_max[slot + v] = run_max[v];
+            lse_den[slot + v] = run_den[v];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Stage 4: population-weighted masses, one workgroup per row:
+//   m_j = sum_s fmaf(n_s, exp2(l_sj - M_s) * (1/D_s), .) * (1 / sum_s n_s).
+
+constexpr int kMassThreads = 256;
+
+__global__ __launch_bounds__(kMassThreads) void masses_kernel(
+    const _Float16* __restrict__ lse, const float* __restrict__ pops,
+    const float* __restrict__ lse_max, const float* __restrict__ lse_den,
+    float* __restrict__ scores, int fb, int64_t ld) {
+    const int64_t row = blockIdx.x;
+    float weight[kCentroids], inv_den[kCentroids], mx[kCentroids];
+    float total = 0.0f;
+#pragma unroll
+    for (int s = 0; s < kCentroids; ++s) {
+        weight[s] = pops[row * kCentroids + s];
+        inv_den[s] = __fdiv_rn(1.0f, lse_den[row * kCentroids + s]);
+        mx[s] = lse_max[row * kCentroids + s];
+        total += weight[s];
+    }
+    const float inv_total = __fdiv_rn(1.0f, total);
+    const _Float16* src = lse + row * kCentroids * ld;
+    float* dst = scores + row * int64_t(fb);
+    typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+    for (int j0 = threadIdx.x * 8; j0 < fb; j0 += kMassThreads * 8) {
+        float score[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) score[e] = 0.0f;
+#pragma unroll
+        for (int s = 0; s < kCentroids; ++s) {
+            const f16x8 h = *reinterpret_cast<const f16x8*>(src + s * ld + j0);
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                score[e] = __builtin_fmaf(weight[s],
+                                          fast_exp2(static_cast<float>(h[e]) - mx[s]) * inv_den[s],
+                                          score[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            if (j0 + e < fb) dst[j0 + e] = score[e] * inv_total;
+    }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Host launchers (validated by the C-ABI layer in api.hip).
+
+int64_t lse_stride(int64_t fb) { return (fb + 63) / 64 * 64; }
+
+int launch_cluster_pool(const void* q, const void* k, int64_t bh, int64_t n, void* centroids,
+                        float* pops, void* pooled, float qk_scale_log2, hipStream_t stream) {
+    const int64_t qb = (n + kQueryBlock - 1) / kQueryBlock;
+    dim3 grid(static_cast<unsigned>(qb), static_cast<unsigned>(bh));
+    hipLaunchKernelGGL(cluster_pool_kernel, grid, dim3(kClusterThreads), 0, stream,
+                       static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                       static_cast<uint16_t*>(centroids), pops, static_cast<uint16_t*>(pooled), n, qb,
+                       qk_scale_log2);
+    return check_launch("cluster_pool_kernel");
+}
+
+int launch_lse(const void* centroids, const void* pooled, int64_t bh, int64_t n, void* lse,
+               float* lse_max, float* lse_den, hipStream_t stream) {
+    const int64_t qb = (n + kQueryBlock - 1) / kQueryBlock;
+    const int64_t fb = n / kKvBlock;
+    const int groups_per_head = static_cast<int>((qb + kLseQBlocks - 1) / kLseQBlocks);
+    const int64_t total = groups_per_head * bh;
+    if (total > (int64_t(1) << 30)) return set_error(1, "ibcs: too many query blocks (%lld)", (long long)total);
+    const int per_xcd = static_cast<int>((total + 7) / 8);
+    const size_t lds = 2 * kLseStageBytes;
+    static bool attr_set = false;
+    if (!attr_set) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(lse_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        attr_set = true;
+    }
+    hipLaunchKernelGGL(lse_kernel, dim3(static_cast<unsigned>(per_xcd * 8)), dim3(kLseThreads), lds, stream,
+                       static_cast<const uint16_t*>(centroids), static_cast<const uint16_t*>(pooled),
+                       static_cast<_Float16*>(lse), lse_max, lse_den, qb, static_cast<int>(fb),
+                       lse_stride(fb), groups_per_head, static_cast<int>(total));
+    return check_launch("lse_kernel");
+}
+
+int launch_masses(const void* lse, const float* pops, const float* lse_max, const float* lse_den,
+                  int64_t rows, int64_t fb, float* scores, hipStream_t stream) {
+    hipLaunchKernelGGL(masses_kernel, dim3(static_cast<unsigned>(rows)), dim3(kMassThreads), 0, stream,
+                       static_cast<const _Float16*>(lse), pops, lse_max, lse_den, scores,
+                       static_cast<int>(fb), lse_stride(fb));
+    return check_launch("masses_kernel");
+}
+
+}  // namespace ab

@@ -1,0 +1,256 @@
+// Weighted paged sparse prefill on gfx950 (bf16 MFMA flash attention).
+//
+// Computes, for every 128-query row of the plan and every valid query i,
+//   z_t = q_i . k_t * log2(e)/sqrt(128) + w_j      (key t in KV4 block j)
+//   o_i = sum_t 2^(z_t - m) v_t / sum_t 2^(z_t - m),  lse_i = m + log2(sum_t 2^(z_t - m))
+// over exactly the row's S sampled KV4 blocks (4S keys). This is the
+// ABSipAttention variant of the reference's FlashInfer prefill
+// (ab_attention/flashinfer_backend.py:30-59): logits + w / (sm_scale*log2 e),
+// then an online softmax in base 2 with scale sm_scale*log2 e.
+//
+// Kernel shape: one workgroup (4 waves) per row; wave w owns queries
+// 32w..32w+31. The row's pages are streamed in tiles of 16 KV4 blocks (64
+// keys): each tile's K rows and transposed V are staged in LDS (double
+// buffered, global loads of tile t+1 in flight while tile t computes).
+//   S^T = K Q^T  : v_mfma_f32_32x32x16_bf16, A = K rows from LDS, B = Q in VGPRs
+//                  -> each lane holds one query and 16 keys per 32-key half,
+//                     in 4-key groups that are exactly one KV4 block.
+//   O^T += V^T P^T: A = V^T rows from LDS, B = P straight from the S^T
+//                  accumulators (bf16), with the key order of each MFMA k-step
+//                  chosen so no cross-lane movement is needed.
+#include "common.hpp"
+
+namespace ab {
+namespace {
+
+constexpr int kPfThreads = 256;
+constexpr int kTilePages = 16;
+constexpr int kTileKeys = kTilePages * kKvBlock;              // 64
+constexpr int kKStageBytes = kTileKeys * kHeadDim * 2;        // 16 KiB
+constexpr int kVStageBytes = kHeadDim * kTileKeys * 2;        // 16 KiB
+constexpr int kStageBytes = kKStageBytes + kVStageBytes + 128; // + weights
+
+// K tile: row = key (0..63), 16 chunks of 16 B, chunk XOR (key & 7).
+__device__ __forceinline__ int k_chunk(int key, int chunk) { return key * 16 + (chunk ^ (key & 7)); }
+// V^T tile: row = dim (0..127), 8 chunks of 16 B (8 keys); chunk XOR (dim & 7).
+__device__ __forceinline__ int v_chunk(int dim, int chunk) { return dim * 8 + (chunk ^ (dim & 7)); }
+// Position of tile page p in a V^T row: within each group of 4 pages the
+// order is {0, 2, 1, 3}, so the two pages one MFMA k-step needs per lane
+// half (p and p+2) are adjacent.
+__device__ __forceinline__ int v_page_pos(int p) {
+    const int u = p & 3;
+    return (p & ~3) | ((u & 1) << 1) | (u >> 1);
+}
+
+__global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const int32_t* __restrict__ ids, const float* __restrict__ logw, uint16_t* __restrict__ out,
+    float* __restrict__ lse, int64_t n, int64_t qb, int64_t rows, int fb, int samples, float scale_log2) {
+    extern __shared__ __align__(16) unsigned char smem[];
+
+    // XCD-aware row order: consecutive rows (neighbouring query blocks of a
+    // head, which share most sampled pages) go to the same XCD's L2.
+    const int64_t hw = blockIdx.x;
+    const int64_t per_xcd = (rows + 7) / 8;
+    const int64_t row = (hw & 7) * per_xcd + (hw >> 3);
+    if (row >= rows) return;
+    const int64_t bh = row / qb, blk = row % qb;
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int qi = lane & 31, half = lane >> 5;
+    const int64_t token = blk * kQueryBlock + wave * 32 + qi;
+    const bool valid_q = token < n;
+
+    // Q as the B operand of S^T = K Q^T: dims 16s + 8*half .. +8.
+    bf16x8 bq[8];
+    {
+        const uint16_t* qrow = q + (bh * n + (valid_q ? token : 0)) * kHeadDim + 8 * half;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            u32x4 val = {0u, 0u, 0u, 0u};
+            if (valid_q) val = *reinterpret_cast<const u32x4*>(qrow + 16 * s);
+            bq[s] = __builtin_bit_cast(bf16x8, val);
+        }
+    }
+
+    const int32_t* row_ids = ids + row * int64_t(samples);
+    const float* row_w = logw + row * int64_t(samples);
+    const u32x4* kbase = reinterpret_cast<const u32x4*>(k + bh * n * kHeadDim);
+    const u32x4* vbase = reinterpret_cast<const u32x4*>(v + bh * n * kHeadDim);
+    const int tiles = samples / kTilePages;
+
+    // Loader role: page lp = tid/16 of the tile, 16-byte chunk lc = tid%16.
+    const int lp = tid >> 4, lc = tid & 15;
+    u32x4 kreg[4], vreg[4];
+    float wreg = 0.f;
+    auto load_tile = [&](int tile) {
+        // Clamp so a malformed plan can never address outside the head.
+        const int64_t j = min(max(row_ids[tile * kTilePages + lp], 0), fb - 1);
+        const int64_t first = (4 * j) * 16 + lc;  // in 16-byte units
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            kreg[i] = kbase[first + 16 * i];
+            vreg[i] = vbase[first + 16 * i];
+        }
+        wreg = row_w[tile * kTilePages + lp];
+    };
+    auto store_tile = [&](unsigned char* st) {
+        u32x4* ks = reinterpret_cast<u32x4*>(st);
+        u32x2* vs = reinterpret_cast<u32x2*>(st + kKStageBytes);
+        float* ws = reinterpret_cast<float*>(st + kKStageBytes + kVStageBytes);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ks[k_chunk(4 * lp + i, lc)] = kreg[i];
+        // Transpose 4 keys x 8 dims into 8 dims x 4 keys (8 bytes each).
+        const int pos = v_page_pos(lp);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t w0 = vreg[0][e], w1 = vreg[1][e], w2 = vreg[2][e], w3 = vreg[3][e];
+            // dim 8*lc + 2e (low halves) and 8*lc + 2e + 1 (high halves)
+            const u32x2 lo = {__builtin_amdgcn_perm(w1, w0, 0x05040100u), __builtin_amdgcn_perm(w3, w2, 0x05040100u)};
+            const u32x2 hi = {__builtin_amdgcn_perm(w1, w0, 0x07060302u), __builtin_amdgcn_perm(w3, w2, 0x07060302u)};
+            const int d0 = 8 * lc + 2 * e, d1 = d0 + 1;
+            vs[2 * v_chunk(d0, pos >> 1) + (pos & 1)] = lo;
+            vs[2 * v_chunk(d1, pos >> 1) + (pos & 1)] = hi;
+        }
+        if (lc == 0) {
+            // weights ordered [half][kt][g] for page 8kt + 2g + half
+            const int h = lp & 1, kt = lp >> 3, g = (lp >> 1) & 3;
+            ws[h * 8 + kt * 4 + g] = wreg;
+        }
+    };
+
+    f32x16 o_acc[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o_acc[dt][r] = 0.f;
+    float m_run = -INFINITY, l_run = 0.f;
+
+    load_tile(0);
+    store_tile(smem);
+    __syncthreads();
+
+    for (int tile = 0; tile < tiles; ++tile) {
+        const bool more = tile + 1 < tiles;
+        if (more) load_tile(tile + 1);
+        const unsigned char* st = smem + (tile & 1) * kStageBytes;
+        const u32x4* ks = reinterpret_cast<const u32x4*>(st);
+        const u32x4* vs = reinterpret_cast<const u32x4*>(st + kKStageBytes);
+        const float* ws = reinterpret_cast<const float*>(st + kKStageBytes + kVStageBytes);
+
+        // S^T for the two 32-key halves.
+        f32x16 sacc[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            f32x16 c;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) c[r] = 0.f;
+            const int key = 32 * kt + qi;
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                const bf16x8 a = __builtin_bit_cast(bf16x8, ks[k_chunk(key, 2 * s + half)]);
+                c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bq[s], c, 0, 0, 0);
+            }
+            sacc[kt] = c;
+        }
+
+        // Logits in base 2 with the block weights; lane register r holds key
+        // 8*(r/4) + 4*half + r%4 of its half, i.e. page 8kt + 2(r/4) + half.
+        float w8[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w8[i] = ws[half * 8 + i];
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float z = __builtin_fmaf(sacc[kt][r], scale_log2, w8[kt * 4 + (r >> 2)]);
+                sacc[kt][r] = z;
+                tmax = fmaxf(tmax, z);
+            }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        const float m_new = fmaxf(m_run, tmax);
+        const float alpha = fast_exp2(m_run - m_new);
+        m_run = m_new;
+        float psum = 0.f;
+        uint32_t pw[2][4][2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                float p[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    p[i] = fast_exp2(sacc[kt][4 * g + i] - m_new);
+                    psum += p[i];
+                }
+                pw[kt][g][0] = pack_bf16(p[0], p[1]);
+                pw[kt][g][1] = pack_bf16(p[2], p[3]);
+            }
+        l_run = l_run * alpha + psum;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o_acc[dt][r] *= alpha;
+
+        // O^T += V^T P^T over 4 k-steps of 16 keys.
+#pragma unroll
+        for (int ks4 = 0; ks4 < 4; ++ks4) {
+            const int kt = ks4 >> 1, g0 = 2 * (ks4 & 1);
+            const u32x4 bw = {pw[kt][g0][0], pw[kt][g0][1], pw[kt][g0 + 1][0], pw[kt][g0 + 1][1]};
+            const bf16x8 b = __builtin_bit_cast(bf16x8, bw);
+            const int group4 = 2 * kt + (ks4 & 1);
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                const int dim = 32 * dt + qi;
+                const bf16x8 a = __builtin_bit_cast(bf16x8, vs[v_chunk(dim, 2 * group4 + half)]);
+                o_acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, o_acc[dt], 0, 0, 0);
+            }
+        }
+
+        if (more) store_tile(smem + ((tile + 1) & 1) * kStageBytes);
+        __syncthreads();
+    }
+
+    const float l_tot = l_run + __shfl_xor(l_run, 32);
+    if (valid_q) {
+        const float inv = 1.0f / l_tot;
+        uint16_t* orow = out + (bh * n + token) * kHeadDim;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const u32x2 pk = {pack_bf16(o_acc[dt][4 * g] * inv, o_acc[dt][4 * g + 1] * inv),
+                                  pack_bf16(o_acc[dt][4 * g + 2] * inv, o_acc[dt][4 * g + 3] * inv)};
+                *reinterpret_cast<u32x2*>(orow + 32 * dt + 8 * g + 4 * half) = pk;
+            }
+        if (lse != nullptr && half == 0) lse[bh * n + token] = m_run + log2f(l_tot);
+    }
+}
+
+}  // namespace
+
+int launch_prefill(const void* q, const void* k, const void* v, int64_t bh, int64_t n, const int32_t* ids,
+                   const float* logw, int64_t samples, void* out, float* lse, hipStream_t stream) {
+    const int64_t qb = (n + kQueryBlock - 1) / kQueryBlock;
+    const int64_t rows = bh * qb;
+    if (samples % kTilePages != 0)
+        return set_error(1, "prefill: samples (%lld) must be a multiple of %d", (long long)samples, kTilePages);
+    const float scale_log2 = static_cast<float>(1.4426950408889634 / 11.313708498984761);  // log2(e)/sqrt(128)
+    const int64_t per_xcd = (rows + 7) / 8;
+    const size_t lds = 2 * kStageBytes;
+    static bool attr_set = false;
+    if (!attr_set) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        attr_set = true;
+    }
+    if (rows == 0) return 0;
+    hipLaunchKernelGGL(prefill_kernel, dim3(static_cast<unsigned>(per_xcd * 8)), dim3(kPfThreads), lds, stream,
+                       static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                       static_cast<const uint16_t*>(v), ids, logw, static_cast<uint16_t*>(out), lse, n, qb, rows,
+                       static_cast<int>(n / kKvBlock), static_cast<int>(samples), scale_log2);
+    return check_launch("prefill_kernel");
+}
+
+}  // namespace ab

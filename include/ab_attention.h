@@ -1,0 +1,93 @@
+/*
+ * C ABI of the MI355X (gfx950) AB-Attention library, libab_attention_hip.so.
+ *
+ * Drop-in boundary for the reference's native ops and its FlashInfer prefill
+ * (paths relative to the reference checkout):
+ *   _C.ibcs(q, k) -> scores          csrc/bindings.cpp:4-5, csrc/ops.h:5, csrc/ibcs.cu:549-617
+ *   _C.sip(scores, offsets, ids, logs)  csrc/bindings.cpp:6-7, csrc/ops.h:7-8, csrc/sip.cu:170-199
+ *   FlashInfer paged prefill run     ab_attention/flashinfer_backend.py:164-242
+ *
+ * Conventions:
+ *   - tensors are plain device pointers, row-major and contiguous, with int64
+ *     sizes; bf16 and fp16 data are passed as raw 16-bit storage;
+ *   - `stream` is a hipStream_t (NULL is the null stream); work is enqueued on
+ *     it, nothing synchronises and nothing allocates: the caller owns every
+ *     buffer, including IBCS workspace sized by ab_ibcs_workspace_bytes();
+ *   - every function returns AB_OK (0) or a nonzero status and then
+ *     ab_last_error() describes the failure (thread local). Validation
+ *     happens before any launch.
+ * Geometry is fixed as in the reference: head dim 128, query blocks of 128
+ * tokens (rows = batch_heads * ceil(tokens / 128)), KV4 blocks of 4 keys
+ * (kv_blocks = tokens / 4), 8 centroids per query block.
+ */
+#ifndef AB_ATTENTION_H
+#define AB_ATTENTION_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AB_ABI_VERSION 1
+
+enum ab_status {
+    AB_OK = 0,
+    AB_ERR_INVALID = 1, /* bad shape, pointer, alignment or size */
+    AB_ERR_LAUNCH = 3   /* the HIP runtime rejected a launch */
+};
+
+/* Message for the last failure on this thread (empty if none). */
+const char *ab_last_error(void);
+int ab_abi_version(void);
+
+/* ---- IBCS: population-weighted KV4 block masses ---------------------------
+ * Replaces _C.ibcs (csrc/ibcs.cu:549-617): q, k bf16 [batch_heads, tokens, 128]
+ * -> scores f32 [rows, kv_blocks], each row summing to 1. `workspace` holds
+ * every intermediate (256-byte aligned, ab_ibcs_workspace_bytes() bytes). */
+size_t ab_ibcs_workspace_bytes(int64_t batch_heads, int64_t tokens);
+int ab_ibcs(const void *q, const void *k, int64_t batch_heads, int64_t tokens, void *workspace,
+            size_t workspace_bytes, float *scores, void *stream);
+
+/* IBCS stages, for callers that keep the intermediates.
+ * cluster_pool (csrc/ibcs.cu:106-266): centroids bf16 [rows, 8, 128], already
+ *   multiplied by 128^-0.5 * log2(e) and rounded to bf16 (csrc/ibcs.cu:293-295);
+ *   populations f32 [rows, 8]; pooled_keys bf16 [batch_heads, kv_blocks, 2, 128].
+ * lse (csrc/ibcs.cu:370-489): block_lse fp16 [rows, 8, ld] with
+ *   ld = ab_ibcs_lse_stride(tokens) >= kv_blocks; lse_max, lse_den f32 [rows, 8].
+ * masses (csrc/ibcs.cu:495-538): scores f32 [rows, kv_blocks]. */
+int64_t ab_ibcs_lse_stride(int64_t tokens);
+int ab_ibcs_cluster_pool(const void *q, const void *k, int64_t batch_heads, int64_t tokens, void *centroids,
+                         float *populations, void *pooled_keys, void *stream);
+int ab_ibcs_lse(const void *centroids, const void *pooled_keys, int64_t batch_heads, int64_t tokens,
+                void *block_lse, float *lse_max, float *lse_den, void *stream);
+int ab_ibcs_masses(const void *block_lse, const float *populations, const float *lse_max, const float *lse_den,
+                   int64_t rows, int64_t kv_blocks, float *scores, void *stream);
+
+/* ---- SIP: systematic inclusion-probability sampling ----------------------
+ * Replaces _C.sip (csrc/sip.cu:170-199): scores f32 [rows, population],
+ * offsets f32 [rows] (uniforms in [0,1)) -> ids int32 [rows, samples] (per-head
+ * KV4 ids: certain blocks first, ascending) and log_weights f32 [rows, samples]
+ * = log2(1/pi). Requires 0 < samples < population. Bit-exact with the
+ * reference algorithm given the same scores and offsets. */
+int ab_sip(const float *scores, const float *offsets, int64_t rows, int64_t population, int64_t samples,
+           int32_t *ids, float *log_weights, void *stream);
+
+/* ---- Weighted paged prefill ------------------------------------------------
+ * Replaces the FlashInfer FA3 run with the ABSipAttention variant
+ * (ab_attention/flashinfer_backend.py:30-59, :164-242): q, k, v bf16
+ * [batch_heads, tokens, 128]; ids/log_weights [rows, samples] (a SamplePlan's
+ * descriptor and log_weights, samples = 32 * sample_pages) -> out bf16
+ * [batch_heads, tokens, 128] and, if lse != NULL, the base-2 log-sum-exp
+ * f32 [batch_heads, tokens]. No page-table translation is needed: ids are
+ * used as per-head KV4 ids directly. */
+int ab_paged_prefill(const void *q, const void *k, const void *v, int64_t batch_heads, int64_t tokens,
+                     const int32_t *ids, const float *log_weights, int64_t samples, void *out, float *lse,
+                     void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AB_ATTENTION_H */
