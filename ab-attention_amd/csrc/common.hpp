@@ -39,8 +39,13 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
     return u >> 16;
 }
 
+// Two floats -> packed bf16 pair with one v_cvt_pk_bf16_f32 (round to nearest
+// even, the same rounding as f32_to_bf16 for every non-NaN input).
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-    return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    const f32x2 v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
 // Hardware base-2 exponential and logarithm (v_exp_f32 / v_log_f32).

@@ -15,9 +15,13 @@
 //   S^T = K Q^T  : v_mfma_f32_32x32x16_bf16, A = K rows from LDS, B = Q in VGPRs
 //                  -> each lane holds one query and 16 keys per 32-key half,
 //                     in 4-key groups that are exactly one KV4 block.
-//   O^T += V^T P^T: A = V^T rows from LDS, B = P straight from the S^T
-//                  accumulators (bf16), with the key order of each MFMA k-step
-//                  chosen so no cross-lane movement is needed.
+//   O^T += V^T P^T: A = V^T read from the row-major V tile with the
+//                  transposing LDS read ds_read_b64_tr_b16, B = P straight
+//                  from the S^T accumulators (bf16); the key order of each
+//                  MFMA k-step is chosen so no cross-lane movement is needed.
+// LDS tiles are row-major [64 keys][128 dims] with rows padded to 272 bytes,
+// which keeps every operand read conflict-free and its address affine in the
+// loop indices (immediate offsets).
 #include "common.hpp"
 
 namespace ab {
@@ -26,20 +30,21 @@ namespace {
 constexpr int kPfThreads = 256;
 constexpr int kTilePages = 16;
 constexpr int kTileKeys = kTilePages * kKvBlock;              // 64
-constexpr int kKStageBytes = kTileKeys * kHeadDim * 2;        // 16 KiB
-constexpr int kVStageBytes = kHeadDim * kTileKeys * 2;        // 16 KiB
-constexpr int kStageBytes = kKStageBytes + kVStageBytes + 128; // + weights
+constexpr int kRowBytes = kHeadDim * 2 + 16;                  // padded row: 272 B
+constexpr int kTileBytes = kTileKeys * kRowBytes;             // 17 KiB
+constexpr int kStageBytes = 2 * kTileBytes + 128;             // K, V, weights
+// Largest p = 2^(y) allowed before the running reference is moved.
+constexpr float kSlack = 8.0f;
 
-// K tile: row = key (0..63), 16 chunks of 16 B, chunk XOR (key & 7).
-__device__ __forceinline__ int k_chunk(int key, int chunk) { return key * 16 + (chunk ^ (key & 7)); }
-// V^T tile: row = dim (0..127), 8 chunks of 16 B (8 keys); chunk XOR (dim & 7).
-__device__ __forceinline__ int v_chunk(int dim, int chunk) { return dim * 8 + (chunk ^ (dim & 7)); }
-// Position of tile page p in a V^T row: within each group of 4 pages the
-// order is {0, 2, 1, 3}, so the two pages one MFMA k-step needs per lane
-// half (p and p+2) are adjacent.
-__device__ __forceinline__ int v_page_pos(int p) {
-    const int u = p & 3;
-    return (p & ~3) | ((u & 1) << 1) | (u >> 1);
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+// Transposing LDS read: within each 16-lane group, lane i receives element
+// i%4 of the 8 bytes read by lanes 4r + i/4, for r = 0..3 (so the group reads
+// a 4 x 16 tile of 16-bit values, row r from lanes 4r..4r+3, and each lane
+// gets one column).
+__device__ __forceinline__ i16x4 lds_read_tr16(const unsigned char* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
 }
 
 __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
@@ -95,27 +100,16 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
         wreg = row_w[tile * kTilePages + lp];
     };
     auto store_tile = [&](unsigned char* st) {
-        u32x4* ks = reinterpret_cast<u32x4*>(st);
-        u32x2* vs = reinterpret_cast<u32x2*>(st + kKStageBytes);
-        float* ws = reinterpret_cast<float*>(st + kKStageBytes + kVStageBytes);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ks[k_chunk(4 * lp + i, lc)] = kreg[i];
-        // Transpose 4 keys x 8 dims into 8 dims x 4 keys (8 bytes each).
-        const int pos = v_page_pos(lp);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const uint32_t w0 = vreg[0][e], w1 = vreg[1][e], w2 = vreg[2][e], w3 = vreg[3][e];
-            // dim 8*lc + 2e (low halves) and 8*lc + 2e + 1 (high halves)
-            const u32x2 lo = {__builtin_amdgcn_perm(w1, w0, 0x05040100u), __builtin_amdgcn_perm(w3, w2, 0x05040100u)};
-            const u32x2 hi = {__builtin_amdgcn_perm(w1, w0, 0x07060302u), __builtin_amdgcn_perm(w3, w2, 0x07060302u)};
-            const int d0 = 8 * lc + 2 * e, d1 = d0 + 1;
-            vs[2 * v_chunk(d0, pos >> 1) + (pos & 1)] = lo;
-            vs[2 * v_chunk(d1, pos >> 1) + (pos & 1)] = hi;
+        for (int i = 0; i < 4; ++i) {
+            const int off = (4 * lp + i) * kRowBytes + 16 * lc;
+            *reinterpret_cast<u32x4*>(st + off) = kreg[i];
+            *reinterpret_cast<u32x4*>(st + kTileBytes + off) = vreg[i];
         }
         if (lc == 0) {
             // weights ordered [half][kt][g] for page 8kt + 2g + half
             const int h = lp & 1, kt = lp >> 3, g = (lp >> 1) & 3;
-            ws[h * 8 + kt * 4 + g] = wreg;
+            reinterpret_cast<float*>(st + 2 * kTileBytes)[h * 8 + kt * 4 + g] = wreg;
         }
     };
 
@@ -124,7 +118,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o_acc[dt][r] = 0.f;
-    float m_run = -INFINITY, l_run = 0.f;
+    float m_run = 0.f, l_run = 0.f;  // reference set by the first tile
 
     load_tile(0);
     store_tile(smem);
@@ -134,9 +128,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
         const bool more = tile + 1 < tiles;
         if (more) load_tile(tile + 1);
         const unsigned char* st = smem + (tile & 1) * kStageBytes;
-        const u32x4* ks = reinterpret_cast<const u32x4*>(st);
-        const u32x4* vs = reinterpret_cast<const u32x4*>(st + kKStageBytes);
-        const float* ws = reinterpret_cast<const float*>(st + kKStageBytes + kVStageBytes);
+        const float* ws = reinterpret_cast<const float*>(st + 2 * kTileBytes);
 
         // S^T for the two 32-key halves.
         f32x16 sacc[2];
@@ -145,10 +137,10 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
             f32x16 c;
 #pragma unroll
             for (int r = 0; r < 16; ++r) c[r] = 0.f;
-            const int key = 32 * kt + qi;
+            const unsigned char* krow = st + (32 * kt + qi) * kRowBytes + 16 * half;
 #pragma unroll
             for (int s = 0; s < 8; ++s) {
-                const bf16x8 a = __builtin_bit_cast(bf16x8, ks[k_chunk(key, 2 * s + half)]);
+                const bf16x8 a = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(krow + 32 * s));
                 c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bq[s], c, 0, 0, 0);
             }
             sacc[kt] = c;
@@ -156,22 +148,38 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
 
         // Logits in base 2 with the block weights; lane register r holds key
         // 8*(r/4) + 4*half + r%4 of its half, i.e. page 8kt + 2(r/4) + half.
-        float w8[8];
+        // Scores are kept relative to the running reference m_run:
+        //   y = s * log2(e)/sqrt(d) + (w - m_run),   p = 2^y.
+        float wm[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) w8[i] = ws[half * 8 + i];
+        for (int i = 0; i < 8; ++i) wm[i] = ws[half * 8 + i] - m_run;
         float tmax = -INFINITY;
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float z = __builtin_fmaf(sacc[kt][r], scale_log2, w8[kt * 4 + (r >> 2)]);
-                sacc[kt][r] = z;
-                tmax = fmaxf(tmax, z);
+                const float y = __builtin_fmaf(sacc[kt][r], scale_log2, wm[kt * 4 + (r >> 2)]);
+                sacc[kt][r] = y;
+                tmax = fmaxf(tmax, y);
             }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        const float m_new = fmaxf(m_run, tmax);
-        const float alpha = fast_exp2(m_run - m_new);
-        m_run = m_new;
+        // Lazy rescaling: the reference moves only when the tile maximum exceeds
+        // it by more than kSlack (so p <= 2^kSlack); the branch is wave-uniform.
+        const bool grow = tile == 0 || tmax > kSlack;
+        if (__any(grow)) {
+            const float shift = grow ? tmax : 0.f;
+            const float alpha = fast_exp2(-shift);
+            m_run += shift;
+            l_run *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o_acc[dt][r] *= alpha;
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sacc[kt][r] -= shift;
+        }
         float psum = 0.f;
         uint32_t pw[2][4][2];
 #pragma unroll
@@ -181,29 +189,32 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
                 float p[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    p[i] = fast_exp2(sacc[kt][4 * g + i] - m_new);
+                    p[i] = fast_exp2(sacc[kt][4 * g + i]);
                     psum += p[i];
                 }
                 pw[kt][g][0] = pack_bf16(p[0], p[1]);
                 pw[kt][g][1] = pack_bf16(p[2], p[3]);
             }
-        l_run = l_run * alpha + psum;
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) o_acc[dt][r] *= alpha;
+        l_run += psum;
 
-        // O^T += V^T P^T over 4 k-steps of 16 keys.
+        // O^T += V^T P^T over 4 k-steps of 16 keys. MFMA k-index 8*half + 4t + r
+        // of k-step ks is key r of tile page 4*ks + 2t + half, on both operands.
+        // A operand of lane (group g = lane/16, i = lane%16): two transposing
+        // reads; the source lane 4r + q addresses key r of that page, dims
+        // 32dt + 16(g%2) + 4q .. +3, so lane i receives dim 32dt + 16(g%2) + i.
+        const unsigned char* vtile = st + kTileBytes + (4 * half + (qi >> 2) % 4) * kRowBytes
+                                     + 32 * ((lane >> 4) & 1) + 8 * (qi & 3);
 #pragma unroll
         for (int ks4 = 0; ks4 < 4; ++ks4) {
             const int kt = ks4 >> 1, g0 = 2 * (ks4 & 1);
             const u32x4 bw = {pw[kt][g0][0], pw[kt][g0][1], pw[kt][g0 + 1][0], pw[kt][g0 + 1][1]};
             const bf16x8 b = __builtin_bit_cast(bf16x8, bw);
-            const int group4 = 2 * kt + (ks4 & 1);
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) {
-                const int dim = 32 * dt + qi;
-                const bf16x8 a = __builtin_bit_cast(bf16x8, vs[v_chunk(dim, 2 * group4 + half)]);
+                const unsigned char* p0 = vtile + (16 * ks4) * kRowBytes + 64 * dt;
+                const i16x4 lo = lds_read_tr16(p0);
+                const i16x4 hi = lds_read_tr16(p0 + 8 * kRowBytes);
+                const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
                 o_acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, o_acc[dt], 0, 0, 0);
             }
         }
