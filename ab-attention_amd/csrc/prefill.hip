@@ -19,9 +19,12 @@
 //                  transposing LDS read ds_read_b64_tr_b16, B = P straight
 //                  from the S^T accumulators (bf16); the key order of each
 //                  MFMA k-step is chosen so no cross-lane movement is needed.
-// LDS tiles are row-major [64 keys][128 dims] with rows padded to 272 bytes,
-// which keeps every operand read conflict-free and its address affine in the
-// loop indices (immediate offsets).
+// LDS tiles (16 KiB each, double buffered) are swizzled so that both the
+// 16-byte stores from the loader and the operand reads are bank-conflict free:
+//   K: [key][16 chunks of 16 B], chunk position = chunk ^ (key & 15);
+//   V: per page 8 blocks of 4 keys x 16 dims (128 B); inside block m the row
+//      of key r sits at position r ^ ((m >> 1) & 3), so each 16-lane group of
+//      a transposing read fetches one whole 128-byte block.
 #include "common.hpp"
 
 namespace ab {
@@ -30,8 +33,7 @@ namespace {
 constexpr int kPfThreads = 256;
 constexpr int kTilePages = 16;
 constexpr int kTileKeys = kTilePages * kKvBlock;              // 64
-constexpr int kRowBytes = kHeadDim * 2 + 16;                  // padded row: 272 B
-constexpr int kTileBytes = kTileKeys * kRowBytes;             // 17 KiB
+constexpr int kTileBytes = kTileKeys * kHeadDim * 2;         // 16 KiB
 constexpr int kStageBytes = 2 * kTileBytes + 128;             // K, V, weights
 // Largest p = 2^(y) allowed before the running reference is moved.
 constexpr float kSlack = 8.0f;
@@ -53,13 +55,18 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
     float* __restrict__ lse, int64_t n, int64_t qb, int64_t rows, int fb, int samples, float scale_log2) {
     extern __shared__ __align__(16) unsigned char smem[];
 
-    // XCD-aware row order: consecutive rows (neighbouring query blocks of a
-    // head, which share most sampled pages) go to the same XCD's L2.
+    // XCD-aware row order. The hardware deals workgroups round-robin over the
+    // 8 XCDs, so workgroup w runs on XCD w % 8. Slot w / 8 walks the heads in
+    // order: at any time all XCDs work on the same head (its K/V stay in the
+    // shared last-level cache), each on a contiguous eighth of its query
+    // blocks (neighbouring blocks share most sampled pages in the XCD's L2).
     const int64_t hw = blockIdx.x;
-    const int64_t per_xcd = (rows + 7) / 8;
-    const int64_t row = (hw & 7) * per_xcd + (hw >> 3);
-    if (row >= rows) return;
-    const int64_t bh = row / qb, blk = row % qb;
+    const int64_t xcd = hw & 7, slot = hw >> 3;
+    const int64_t per_xcd = (qb + 7) / 8;
+    const int64_t bh = slot / per_xcd;
+    const int64_t blk = xcd * per_xcd + slot % per_xcd;
+    if (bh >= rows / qb || blk >= qb) return;
+    const int64_t row = bh * qb + blk;
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int qi = lane & 31, half = lane >> 5;
@@ -99,12 +106,15 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
         }
         wreg = row_w[tile * kTilePages + lp];
     };
+    // Loader's LDS offsets (key 4*lp + i, 16-byte chunk lc).
+    const int v_store = lp * 1024 + (lc >> 1) * 128 + (lc & 1) * 16;
+    const int v_swz = (lc >> 2) & 3;  // (block >> 1) & 3 with block = lc >> 1
     auto store_tile = [&](unsigned char* st) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int off = (4 * lp + i) * kRowBytes + 16 * lc;
-            *reinterpret_cast<u32x4*>(st + off) = kreg[i];
-            *reinterpret_cast<u32x4*>(st + kTileBytes + off) = vreg[i];
+            const int key = 4 * lp + i;
+            *reinterpret_cast<u32x4*>(st + key * 256 + 16 * (lc ^ (key & 15))) = kreg[i];
+            *reinterpret_cast<u32x4*>(st + kTileBytes + v_store + 32 * (i ^ v_swz)) = vreg[i];
         }
         if (lc == 0) {
             // weights ordered [half][kt][g] for page 8kt + 2g + half
@@ -112,6 +122,18 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
             reinterpret_cast<float*>(st + 2 * kTileBytes)[h * 8 + kt * 4 + g] = wreg;
         }
     };
+
+    // Operand-read offsets of this lane (stage-relative).
+    int k_off[8];  // S^T A operand: key qi (+32kt), chunk 2s + half
+#pragma unroll
+    for (int s8 = 0; s8 < 8; ++s8) k_off[s8] = qi * 256 + 16 * ((2 * s8 + half) ^ (qi & 15));
+    int v_off[4];  // PV A operand, transposing read: page half (+4ks + 2t), block 2dt + (lane>>4)&1
+    {
+        const int gd = (lane >> 4) & 1, r = (lane >> 2) & 3, q = lane & 3;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+            v_off[dt] = kTileBytes + half * 1024 + (2 * dt + gd) * 128 + 32 * (r ^ dt) + 8 * q;
+    }
 
     f32x16 o_acc[4];
 #pragma unroll
@@ -137,10 +159,10 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
             f32x16 c;
 #pragma unroll
             for (int r = 0; r < 16; ++r) c[r] = 0.f;
-            const unsigned char* krow = st + (32 * kt + qi) * kRowBytes + 16 * half;
 #pragma unroll
             for (int s = 0; s < 8; ++s) {
-                const bf16x8 a = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(krow + 32 * s));
+                const bf16x8 a = __builtin_bit_cast(
+                    bf16x8, *reinterpret_cast<const u32x4*>(st + k_off[s] + kt * 32 * 256));
                 c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bq[s], c, 0, 0, 0);
             }
             sacc[kt] = c;
@@ -202,8 +224,6 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
         // A operand of lane (group g = lane/16, i = lane%16): two transposing
         // reads; the source lane 4r + q addresses key r of that page, dims
         // 32dt + 16(g%2) + 4q .. +3, so lane i receives dim 32dt + 16(g%2) + i.
-        const unsigned char* vtile = st + kTileBytes + (4 * half + (qi >> 2) % 4) * kRowBytes
-                                     + 32 * ((lane >> 4) & 1) + 8 * (qi & 3);
 #pragma unroll
         for (int ks4 = 0; ks4 < 4; ++ks4) {
             const int kt = ks4 >> 1, g0 = 2 * (ks4 & 1);
@@ -211,9 +231,9 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
             const bf16x8 b = __builtin_bit_cast(bf16x8, bw);
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) {
-                const unsigned char* p0 = vtile + (16 * ks4) * kRowBytes + 64 * dt;
+                const unsigned char* p0 = st + v_off[dt] + ks4 * 4096;
                 const i16x4 lo = lds_read_tr16(p0);
-                const i16x4 hi = lds_read_tr16(p0 + 8 * kRowBytes);
+                const i16x4 hi = lds_read_tr16(p0 + 2048);
                 const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
                 o_acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, o_acc[dt], 0, 0, 0);
             }
@@ -248,7 +268,7 @@ int launch_prefill(const void* q, const void* k, const void* v, int64_t bh, int6
     if (samples % kTilePages != 0)
         return set_error(1, "prefill: samples (%lld) must be a multiple of %d", (long long)samples, kTilePages);
     const float scale_log2 = static_cast<float>(1.4426950408889634 / 11.313708498984761);  // log2(e)/sqrt(128)
-    const int64_t per_xcd = (rows + 7) / 8;
+    const int64_t per_xcd = (qb + 7) / 8;
     const size_t lds = 2 * kStageBytes;
     static bool attr_set = false;
     if (!attr_set) {
@@ -257,7 +277,7 @@ int launch_prefill(const void* q, const void* k, const void* v, int64_t bh, int6
         attr_set = true;
     }
     if (rows == 0) return 0;
-    hipLaunchKernelGGL(prefill_kernel, dim3(static_cast<unsigned>(per_xcd * 8)), dim3(kPfThreads), lds, stream,
+    hipLaunchKernelGGL(prefill_kernel, dim3(static_cast<unsigned>(per_xcd * 8 * bh)), dim3(kPfThreads), lds, stream,
                        static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                        static_cast<const uint16_t*>(v), ids, logw, static_cast<uint16_t*>(out), lse, n, qb, rows,
                        static_cast<int>(n / kKvBlock), static_cast<int>(samples), scale_log2);

@@ -108,6 +108,8 @@ def main() -> int:
     ap.add_argument("--heads", type=int, default=None, help="override head count (profiling only)")
     ap.add_argument("--cpu-sample-rows", type=int, default=8)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 1 GiB device-to-device copy (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: every GPU box here has one GPU, and the path shards by "
@@ -115,6 +117,15 @@ def main() -> int:
         return 2
 
     import torch
+
+    if args.copy_calibration:
+        src = torch.empty(1 << 28, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_each_way": src.numel() * 4, "launches": 3}))
+        return 0
 
     from ab_attention import apply_plan, build_plan
     from ab_attention.synthetic import CONFIGS, make_qkv
