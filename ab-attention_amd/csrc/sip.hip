@@ -14,163 +14,215 @@
 // contracts it); every other product is rounded before its sum, which the
 // build enforces with -ffp-contract=off.
 //
-// Row storage: when the row fits, the clamped masses live in LDS with the
-// certainty mark in their sign (as the reference does); otherwise they are
-// re-read from global memory and certainty is an LDS bitmask. Both give the
-// same bits.
+// Workgroups have 1024 threads (16 waves) per row. The 256 "logical threads"
+// that define CUB's association (threads 0..255) own the ordered folds and
+// the chunk chains; the association-free phases (staging, marking, the last
+// residual, the draws) use all 1024 threads, which keeps enough waves per
+// SIMD to hide LDS and fp64 latency.
+//
+// Two storage schemes, same bits:
+//   - sip_lds_kernel (rows whose clamped masses and fp64 prefixes fit in LDS):
+//     persistent workgroups walk rows r, r + grid, ...; while a row is
+//     processed out of LDS, the next row's masses are already being loaded
+//     into registers in the thread-strided order of the first certainty
+//     pass, so that pass folds straight from registers. Certainty is marked
+//     by negating the LDS copy, as the reference does.
+//   - sip_global_kernel (larger rows): one row per workgroup, the row is
+//     re-read from L2 by each pass, LDS holds the prefixes and a certainty
+//     bitmask.
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace ab {
 namespace {
 
-constexpr int kSipThreads = 256;
+constexpr int kSipThreads = 256;   // logical threads of the reference's CUB blocks
+constexpr int kSipWorkers = 1024;  // hardware threads per row
 constexpr int kBucket = 4;
+constexpr int kUnroll = 8;
+constexpr int kDraws = 2;
 
-template <bool kLdsValues>
-struct RowView {
+// Clamped masses held in LDS; the sign marks certainty.
+struct LdsRow {
     const float* input;
-    float* values;      // LDS copy (kLdsValues)
-    uint32_t* marks;    // LDS bitmask (!kLdsValues)
-
-    __device__ __forceinline__ float x(int i) const {
-        if constexpr (kLdsValues) return fabsf(values[i]);
-        else return fmaxf(input[i], 1e-30f);
-    }
-    __device__ __forceinline__ bool certain(int i) const {
-        if constexpr (kLdsValues) return values[i] < 0.f;
-        else return (marks[i >> 5] >> (i & 31)) & 1u;
-    }
-    __device__ __forceinline__ void mark(int i) {
-        if constexpr (kLdsValues) values[i] = -values[i];
-        else atomicOr(&marks[i >> 5], 1u << (i & 31));
-    }
+    float* values;
+    __device__ __forceinline__ float x(int i) const { return fabsf(values[i]); }
+    __device__ __forceinline__ bool certain(int i) const { return values[i] < 0.f; }
+    __device__ __forceinline__ void mark(int i) { values[i] = -values[i]; }
+    __device__ __forceinline__ void set_any_certain(bool) {}
 };
 
-template <bool kLdsValues>
-__global__ __launch_bounds__(kSipThreads) void sip_kernel(
-    const float* __restrict__ masses, const float* __restrict__ offsets,
-    int32_t* __restrict__ ids, float* __restrict__ logw, int population, int samples) {
-    extern __shared__ __align__(16) unsigned char smem[];
-    __shared__ double part[kSipThreads];
-    __shared__ double group_max[kSipThreads / 32];
-    __shared__ double s_scale;
-    __shared__ int s_new, s_pass, s_last;
-    __shared__ int s_count[kSipThreads];
-
-    const int t = threadIdx.x;
-    const int64_t row = blockIdx.x;
-    const int pop = population;
-    const int buckets = (pop + kBucket - 1) / kBucket;
-    double* prefix = reinterpret_cast<double*>(smem);
-    const int mask_words = (pop + 31) / 32;
-    RowView<kLdsValues> rv;
-    rv.input = masses + row * int64_t(pop);
-    rv.marks = reinterpret_cast<uint32_t*>(prefix + buckets + 1);
-    rv.values = reinterpret_cast<float*>(rv.marks + mask_words);
-
-    if constexpr (kLdsValues) {
-        for (int i = t; i < pop; i += kSipThreads) rv.values[i] = fmaxf(rv.input[i], 1e-30f);
-    } else {
-        for (int w = t; w < mask_words; w += kSipThreads) rv.marks[w] = 0u;
+// Raw masses in global memory, certainty in an LDS bitmask.
+struct GlobalRow {
+    const float* input;
+    uint32_t* marks;
+    bool any_certain;
+    __device__ __forceinline__ float x(int i) const { return fmaxf(input[i], 1e-30f); }
+    __device__ __forceinline__ bool certain(int i) const {
+        return any_certain && ((marks[i >> 5] >> (i & 31)) & 1u);
     }
-    __syncthreads();
+    __device__ __forceinline__ void mark(int i) { atomicOr(&marks[i >> 5], 1u << (i & 31)); }
+    __device__ __forceinline__ void set_any_certain(bool v) { any_certain = v; }
+};
+
+struct SipShared {
+    double part[kSipThreads];
+    double group_max[kSipThreads / 32];
+    double scale;
+    int added, pass, last;
+    int wave_count[kSipThreads / 64];
+};
+
+// Thread-strided partial (sum, max) over the non-certain masses: thread t
+// folds i = t, t+256, ... in order (sip.cu:63-71).
+template <class R>
+__device__ __forceinline__ void strided_partials(const R& rv, int pop, double& sum, double& mx) {
+    const int t = threadIdx.x;
+    sum = 0.0;
+    mx = 0.0;
+    for (int i0 = t; i0 < pop; i0 += kSipThreads * kUnroll) {
+        float v[kUnroll];
+#pragma unroll
+        for (int e = 0; e < kUnroll; ++e) {
+            const int i = i0 + e * kSipThreads;
+            v[e] = (i < pop && !rv.certain(i)) ? rv.x(i) : -1.0f;
+        }
+#pragma unroll
+        for (int e = 0; e < kUnroll; ++e)
+            if (v[e] >= 0.0f) {
+                const double d = static_cast<double>(v[e]);
+                sum = sum + d;
+                mx = fmax(mx, d);
+            }
+    }
+}
+
+// Everything after the first pass's thread partials are known: certainty
+// iteration, certain ids, chunk scan, bucket prefixes and the draws.
+template <class R>
+__device__ void sip_row(R& rv, double sum, double mx, double* prefix, SipShared& sh, float offset_u,
+                        int32_t* __restrict__ out_ids, float* __restrict__ out_w, int pop, int samples) {
+    const int t = threadIdx.x;
+    const bool logical = t < kSipThreads;
+    const int buckets = (pop + kBucket - 1) / kBucket;
 
     // Certainty passes (sip.cu:62-96).
     int certainty = 0;
     double scale;
-    for (;;) {
-        double sum = 0.0, mx = 0.0;
-        for (int i = t; i < pop; i += kSipThreads)
-            if (!rv.certain(i)) {
-                const double v = static_cast<double>(rv.x(i));
-                sum = sum + v;
-                mx = fmax(mx, v);
-            }
+    for (int pass = 0;; ++pass) {
+        if (logical) {
+            if (pass > 0) strided_partials(rv, pop, sum, mx);
 #pragma unroll
-        for (int off = 1; off < 32; off <<= 1) {
-            const double os = __shfl_down(sum, off, 32);
-            const double om = __shfl_down(mx, off, 32);
-            sum = sum + os;
-            mx = fmax(mx, om);
-        }
-        if ((t & 31) == 0) {
-            part[t >> 5] = sum;
-            group_max[t >> 5] = mx;
+            for (int off = 1; off < 32; off <<= 1) {
+                const double os = __shfl_down(sum, off, 32);
+                const double om = __shfl_down(mx, off, 32);
+                sum = sum + os;
+                mx = fmax(mx, om);
+            }
+            if ((t & 31) == 0) {
+                sh.part[t >> 5] = sum;
+                sh.group_max[t >> 5] = mx;
+            }
         }
         __syncthreads();
         if (t == 0) {
-            double total = part[0], maximum = group_max[0];
+            double total = sh.part[0], maximum = sh.group_max[0];
             for (int w = 1; w < kSipThreads / 32; ++w) {
-                total = total + part[w];
-                maximum = fmax(maximum, group_max[w]);
+                total = total + sh.part[w];
+                maximum = fmax(maximum, sh.group_max[w]);
             }
             const double sc = static_cast<double>(samples - certainty) / total;
-            s_scale = sc;
-            s_pass = maximum * sc >= 1.0;
-            s_new = 0;
+            sh.scale = sc;
+            sh.pass = maximum * sc >= 1.0;
+            sh.added = 0;
         }
         __syncthreads();
-        scale = s_scale;
-        if (s_pass) {
+        scale = sh.scale;
+        if (sh.pass) {
             int count = 0;
-            for (int i = t; i < pop; i += kSipThreads)
+            for (int i = t; i < pop; i += kSipWorkers)
                 if (!rv.certain(i) && static_cast<double>(rv.x(i)) * scale >= 1.0) {
                     rv.mark(i);
                     ++count;
                 }
-            if (count) atomicAdd(&s_new, count);
+            if (count) atomicAdd(&sh.added, count);
         }
         __syncthreads();
-        const int added = s_new;
+        const int added = sh.added;
         certainty += added;
+        rv.set_any_certain(certainty != 0);
         __syncthreads();
         if (added == 0) break;
     }
 
-    // Last residual (non-certain) index; a max is order independent.
-    if (t == 0) s_last = -1;
-    __syncthreads();
-    {
-        int last = -1;
-        for (int i = t; i < pop; i += kSipThreads)
-            if (!rv.certain(i)) last = i;
-        if (last >= 0) atomicMax(&s_last, last);
+    // Last residual (non-certain) index: the last element unless marked.
+    int last = pop - 1;
+    if (certainty != 0) {
+        if (t == 0) sh.last = -1;
+        __syncthreads();
+        int mine = -1;
+        for (int i = t; i < pop; i += kSipWorkers)
+            if (!rv.certain(i)) mine = i;
+        if (mine >= 0) atomicMax(&sh.last, mine);
+        __syncthreads();
+        last = sh.last;
     }
-    __syncthreads();
-    const int last = s_last;
 
     const int chunk = ((buckets + kSipThreads - 1) / kSipThreads) * kBucket;  // sip.cu:99-101
     const int begin = t * chunk;
-    const int end = min(begin + chunk, pop);
-    int32_t* out_ids = ids + row * int64_t(samples);
-    float* out_w = logw + row * int64_t(samples);
+    const int end = logical ? min(begin + chunk, pop) : begin;
 
-    // Certain ids first, ascending, weight 0 (sip.cu:108-124).
+    // Certain ids first, ascending, weight 0 (sip.cu:108-124): chunk counts,
+    // an exclusive scan over the 256 chunks (integer, order free), then
+    // each chunk writes its certain ids in order.
     if (certainty != 0) {
         int count = 0;
         for (int i = begin; i < end; ++i) count += rv.certain(i);
-        s_count[t] = count;
-        __syncthreads();
-        int slot = 0;
-        for (int u = 0; u < t; ++u) slot += s_count[u];
-        for (int i = begin; i < end; ++i)
-            if (rv.certain(i)) {
-                out_ids[slot] = i;
-                out_w[slot++] = 0.f;
+        int inc = count;
+        if (logical) {
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const int o = __shfl_up(inc, off);
+                if ((t & 63) >= off) inc += o;
             }
+            if ((t & 63) == 63) sh.wave_count[t >> 6] = inc;
+        }
+        __syncthreads();
+        if (logical) {
+            int slot = inc - count;
+            for (int w = 0; w < (t >> 6); ++w) slot += sh.wave_count[w];
+            for (int i = begin; i < end; ++i)
+                if (rv.certain(i)) {
+                    out_ids[slot] = i;
+                    out_w[slot++] = 0.f;
+                }
+        }
         __syncthreads();
     }
 
     // Chunk masses and their CUB-ordered exclusive scan (sip.cu:126-130).
-    double chunk_mass = 0.0;
-    for (int i = begin; i < end; ++i)
-        chunk_mass = chunk_mass + (rv.certain(i) ? 0.0 : static_cast<double>(rv.x(i)) * scale);
-    part[t] = chunk_mass;
+    if (logical) {
+        double chunk_mass = 0.0;
+        for (int i0 = begin; i0 < end; i0 += kUnroll) {
+            float v[kUnroll];
+#pragma unroll
+            for (int e = 0; e < kUnroll; ++e) {
+                const int i = i0 + e;
+                v[e] = (i < end && !rv.certain(i)) ? rv.x(i) : -1.0f;
+            }
+#pragma unroll
+            for (int e = 0; e < kUnroll; ++e)
+                if (i0 + e < end)
+                    chunk_mass = chunk_mass + (v[e] < 0.0f ? 0.0 : static_cast<double>(v[e]) * scale);
+        }
+        sh.part[t] = chunk_mass;
+    }
     __syncthreads();
     if (t < 32) {
-        double seg = part[8 * t];
+        double seg = sh.part[8 * t];
 #pragma unroll
-        for (int i = 1; i < 8; ++i) seg = seg + part[8 * t + i];
+        for (int i = 1; i < 8; ++i) seg = seg + sh.part[8 * t + i];
         double inc = seg;
 #pragma unroll
         for (int off = 1; off < 32; off <<= 1) {
@@ -182,82 +234,196 @@ __global__ __launch_bounds__(kSipThreads) void sip_kernel(
         double ex = (t == 0) ? 0.0 : up;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const double in = part[8 * t + i];
-            part[8 * t + i] = ex;
+            const double in = sh.part[8 * t + i];
+            sh.part[8 * t + i] = ex;
             ex = ex + in;
         }
     }
     __syncthreads();
-    double cumulative = part[t];
 
     // Bucket prefixes (sip.cu:131-142).
     const int residuals = samples - certainty;
     if (t == 0) prefix[buckets] = static_cast<double>(residuals);
-    for (int i = begin; i < end; ++i) {
-        if (i % kBucket == 0) prefix[i / kBucket] = i > last ? static_cast<double>(residuals) : cumulative;
-        cumulative = cumulative + (rv.certain(i) ? 0.0 : static_cast<double>(rv.x(i)) * scale);
+    if (logical) {
+        double cumulative = sh.part[t];
+        for (int i0 = begin; i0 < end; i0 += kUnroll) {
+            float v[kUnroll];
+#pragma unroll
+            for (int e = 0; e < kUnroll; ++e) {
+                const int i = i0 + e;
+                v[e] = (i < end && !rv.certain(i)) ? rv.x(i) : -1.0f;
+            }
+#pragma unroll
+            for (int e = 0; e < kUnroll; ++e) {
+                const int i = i0 + e;
+                if (i < end) {
+                    if (i % kBucket == 0)
+                        prefix[i / kBucket] = i > last ? static_cast<double>(residuals) : cumulative;
+                    cumulative = cumulative + (v[e] < 0.0f ? 0.0 : static_cast<double>(v[e]) * scale);
+                }
+            }
+        }
     }
     __syncthreads();
 
-    // Systematic draws (sip.cu:144-166).
-    const double offset = static_cast<double>(offsets[row]);
-    for (int slot = t; slot < residuals; slot += kSipThreads) {
-        const double threshold = offset + static_cast<double>(slot);
-        int lower = 0, upper = buckets;
-        while (lower < upper) {
-            const int middle = (lower + upper + 1) / 2;
-            if (prefix[middle] <= threshold) lower = middle;
-            else upper = middle - 1;
+    // Systematic draws (sip.cu:144-166). Each thread runs up to kDraws
+    // independent searches in lockstep (their LDS reads overlap); every search
+    // makes exactly the reference's probes.
+    const double offset = static_cast<double>(offset_u);
+    for (int slot0 = t; slot0 < residuals; slot0 += kSipWorkers * kDraws) {
+        int lower[kDraws], upper[kDraws];
+        double threshold[kDraws];
+#pragma unroll
+        for (int d = 0; d < kDraws; ++d) {
+            const int slot = slot0 + d * kSipWorkers;
+            threshold[d] = offset + static_cast<double>(slot);
+            lower[d] = 0;
+            upper[d] = slot < residuals ? buckets : 0;
         }
-        const int bucket = min(lower, buckets - 1);
-        double mass = prefix[bucket];
-        int selected = last;
-        const int stop = min((bucket + 1) * kBucket, pop);
-        for (int i = bucket * kBucket; i < stop; ++i) {
-            if (rv.certain(i)) continue;
-            selected = i;
-            mass = fma(static_cast<double>(rv.x(i)), scale, mass);
-            if (mass > threshold) break;
+        bool busy = true;
+        while (busy) {
+            busy = false;
+#pragma unroll
+            for (int d = 0; d < kDraws; ++d)
+                if (lower[d] < upper[d]) {
+                    const int middle = (lower[d] + upper[d] + 1) / 2;
+                    if (prefix[middle] <= threshold[d]) lower[d] = middle;
+                    else upper[d] = middle - 1;
+                    busy = true;
+                }
         }
-        out_ids[certainty + slot] = selected;
-        out_w[certainty + slot] =
-            static_cast<float>(-log2(fmax(static_cast<double>(rv.input[selected]), 1e-30) * scale));
+#pragma unroll
+        for (int d = 0; d < kDraws; ++d) {
+            const int slot = slot0 + d * kSipWorkers;
+            if (slot >= residuals) continue;
+            const int bucket = min(lower[d], buckets - 1);
+            double mass = prefix[bucket];
+            int selected = last;
+            const int stop = min((bucket + 1) * kBucket, pop);
+            for (int i = bucket * kBucket; i < stop; ++i) {
+                if (rv.certain(i)) continue;
+                selected = i;
+                mass = fma(static_cast<double>(rv.x(i)), scale, mass);
+                if (mass > threshold[d]) break;
+            }
+            out_ids[certainty + slot] = selected;
+            out_w[certainty + slot] =
+                static_cast<float>(-log2(fmax(static_cast<double>(rv.input[selected]), 1e-30) * scale));
+        }
     }
+}
+
+// Persistent kernel, row in LDS. Each of the 1024 threads prefetches up to
+// kPer >= ceil(population / 1024) masses of the next row into registers.
+template <int kPer>
+__global__ __launch_bounds__(kSipWorkers) void sip_lds_kernel(
+    const float* __restrict__ masses, const float* __restrict__ offsets, int32_t* __restrict__ ids,
+    float* __restrict__ logw, int population, int samples, int64_t rows) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ SipShared sh;
+    const int t = threadIdx.x;
+    const int pop = population;
+    const int buckets = (pop + kBucket - 1) / kBucket;
+    double* prefix = reinterpret_cast<double*>(smem);
+    float* values = reinterpret_cast<float*>(prefix + buckets + 1);
+
+    float next[kPer];
+    auto prefetch = [&](int64_t r) {
+        const float* in = masses + r * int64_t(pop);
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int i = t + k * kSipWorkers;
+            next[k] = i < pop ? in[i] : 0.0f;
+        }
+    };
+    int64_t row = blockIdx.x;
+    if (row < rows) prefetch(row);
+    for (; row < rows; row += gridDim.x) {
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int i = t + k * kSipWorkers;
+            if (i < pop) values[i] = fmaxf(next[k], 1e-30f);
+        }
+        const int64_t following = row + gridDim.x;
+        if (following < rows) prefetch(following);
+        __syncthreads();
+        LdsRow rv{masses + row * int64_t(pop), values};
+        double sum = 0.0, mx = 0.0;
+        if (t < kSipThreads) strided_partials(rv, pop, sum, mx);
+        sip_row(rv, sum, mx, prefix, sh, offsets[row], ids + row * int64_t(samples),
+                logw + row * int64_t(samples), pop, samples);
+        __syncthreads();  // the next row overwrites values and prefixes
+    }
+}
+
+__global__ __launch_bounds__(kSipWorkers) void sip_global_kernel(
+    const float* __restrict__ masses, const float* __restrict__ offsets, int32_t* __restrict__ ids,
+    float* __restrict__ logw, int population, int samples) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ SipShared sh;
+    const int t = threadIdx.x;
+    const int64_t row = blockIdx.x;
+    const int pop = population;
+    const int buckets = (pop + kBucket - 1) / kBucket;
+    double* prefix = reinterpret_cast<double*>(smem);
+    GlobalRow rv{masses + row * int64_t(pop), reinterpret_cast<uint32_t*>(prefix + buckets + 1), false};
+    for (int w = t; w < (pop + 31) / 32; w += kSipWorkers) rv.marks[w] = 0u;
+    __syncthreads();
+    double sum = 0.0, mx = 0.0;
+    if (t < kSipThreads) strided_partials(rv, pop, sum, mx);
+    sip_row(rv, sum, mx, prefix, sh, offsets[row], ids + row * int64_t(samples), logw + row * int64_t(samples),
+            pop, samples);
+}
+
+template <int kPer>
+int launch_lds(const float* scores, const float* offsets, int64_t rows, int pop, int samples, int32_t* ids,
+               float* logw, size_t bytes, hipStream_t stream) {
+    const void* fn = reinterpret_cast<const void*>(sip_lds_kernel<kPer>);
+    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+    int device = 0, cus = 0, per_cu = 0;
+    (void)hipGetDevice(&device);
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kSipWorkers, bytes) != hipSuccess || per_cu < 1)
+        per_cu = 1;
+    const int64_t grid = std::min<int64_t>(rows, int64_t(std::max(cus, 1)) * per_cu);
+    hipLaunchKernelGGL(sip_lds_kernel<kPer>, dim3(static_cast<unsigned>(grid)), dim3(kSipWorkers), bytes, stream,
+                       scores, offsets, ids, logw, pop, samples, rows);
+    return check_launch("sip_lds_kernel");
 }
 
 }  // namespace
 
+constexpr size_t kSipStaticLds = sizeof(SipShared);
+constexpr size_t kLdsLimit = 160 * 1024;
+
 size_t sip_lds_bytes(int64_t population, bool lds_values) {
     const int64_t buckets = (population + kBucket - 1) / kBucket;
-    const int64_t words = (population + 31) / 32;
-    size_t bytes = size_t(buckets + 1) * 8 + size_t(words) * 4;
-    if (lds_values) bytes += size_t(population) * 4;
-    return bytes;
+    const size_t base = size_t(buckets + 1) * 8;
+    return lds_values ? base + size_t(population) * 4 : base + size_t((population + 31) / 32) * 4;
 }
-
-// Static LDS of sip_kernel: part (2 KiB) + group_max + scalars + s_count (1 KiB).
-constexpr size_t kSipStaticLds = kSipThreads * 8 + 8 * 8 + 8 + 12 + kSipThreads * 4;
-constexpr size_t kLdsLimit = 160 * 1024;
 
 bool sip_fits(int64_t population) { return sip_lds_bytes(population, false) + kSipStaticLds <= kLdsLimit; }
 
 int launch_sip(const float* scores, const float* offsets, int64_t rows, int64_t population, int64_t samples,
                int32_t* ids, float* logw, hipStream_t stream) {
-    const bool lds_values = sip_lds_bytes(population, true) + kSipStaticLds <= kLdsLimit;
-    const size_t bytes = sip_lds_bytes(population, lds_values);
-    if (bytes + kSipStaticLds > kLdsLimit)
+    if (!sip_fits(population))
         return set_error(1, "sip: population %lld exceeds single-workgroup LDS capacity", (long long)population);
-    const void* fn = lds_values ? reinterpret_cast<const void*>(sip_kernel<true>)
-                                : reinterpret_cast<const void*>(sip_kernel<false>);
-    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
     if (rows == 0) return 0;
-    if (lds_values)
-        hipLaunchKernelGGL(sip_kernel<true>, dim3(static_cast<unsigned>(rows)), dim3(kSipThreads), bytes, stream,
-                           scores, offsets, ids, logw, static_cast<int>(population), static_cast<int>(samples));
-    else
-        hipLaunchKernelGGL(sip_kernel<false>, dim3(static_cast<unsigned>(rows)), dim3(kSipThreads), bytes, stream,
-                           scores, offsets, ids, logw, static_cast<int>(population), static_cast<int>(samples));
-    return check_launch("sip_kernel");
+    const int pop = static_cast<int>(population), s = static_cast<int>(samples);
+    const size_t lds_bytes = sip_lds_bytes(population, true);
+    const int per_thread = (pop + kSipWorkers - 1) / kSipWorkers;
+    if (lds_bytes + kSipStaticLds <= kLdsLimit) {
+        if (per_thread <= 4) return launch_lds<4>(scores, offsets, rows, pop, s, ids, logw, lds_bytes, stream);
+        if (per_thread <= 8) return launch_lds<8>(scores, offsets, rows, pop, s, ids, logw, lds_bytes, stream);
+        if (per_thread <= 16) return launch_lds<16>(scores, offsets, rows, pop, s, ids, logw, lds_bytes, stream);
+        if (per_thread <= 24) return launch_lds<24>(scores, offsets, rows, pop, s, ids, logw, lds_bytes, stream);
+    }
+    const size_t bytes = sip_lds_bytes(population, false);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(sip_global_kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+    hipLaunchKernelGGL(sip_global_kernel, dim3(static_cast<unsigned>(rows)), dim3(kSipWorkers), bytes, stream,
+                       scores, offsets, ids, logw, pop, s);
+    return check_launch("sip_global_kernel");
 }
 
 }  // namespace ab
