@@ -1,0 +1,81 @@
+"""The Python surface keeps the reference's names, defaults and validation
+(ab_attention/attention.py:26-102, flashinfer_backend.py:164-193; the native
+op checks of csrc/ibcs.cu:550-568 and csrc/sip.cu:172-192). CPU only: every
+check here fires before any launch."""
+import inspect
+
+import pytest
+import torch
+
+import ab_attention
+from ab_attention import SamplePlan, _C, ab_attention as ab_attn, apply_plan, build_plan
+from ab_attention.flashinfer_backend import paged_attention
+
+
+def test_public_names_and_defaults():
+    assert ab_attention.__all__ == ["SamplePlan", "ab_attention", "apply_plan", "build_plan"]
+    assert SamplePlan._fields == ("descriptor", "log_weights")
+    sig = inspect.signature(build_plan)
+    assert sig.parameters["sample_pages"].default == 64 and sig.parameters["seed"].default == 42
+    assert inspect.signature(apply_plan).parameters["return_lse"].default is False
+    assert inspect.signature(ab_attn).parameters["sample_pages"].default == 64
+    assert inspect.signature(paged_attention).parameters["return_lse"].default is False
+
+
+def _qk(shape=(1, 2, 1024, 128), dtype=torch.bfloat16):
+    return torch.zeros(shape, dtype=dtype), torch.zeros(shape, dtype=dtype)
+
+
+@pytest.mark.parametrize("shape_q,shape_k,pages,msg", [
+    ((2, 1024, 128), (2, 1024, 128), 1, "N divisible by 4"),
+    ((1, 2, 1024, 128), (1, 2, 1020, 128), 1, "N divisible by 4"),
+    ((1, 2, 1022, 128), (1, 2, 1022, 128), 1, "N divisible by 4"),
+    ((1, 2, 1024, 128), (1, 2, 1024, 128), 0, "positive"),
+    ((1, 2, 1024, 128), (1, 2, 1024, 128), 8, "smaller than the sequence"),
+])
+def test_build_plan_value_errors(shape_q, shape_k, pages, msg):
+    with pytest.raises(ValueError, match=msg):
+        build_plan(torch.zeros(shape_q, dtype=torch.bfloat16), torch.zeros(shape_k, dtype=torch.bfloat16),
+                   sample_pages=pages)
+
+
+def test_build_plan_rejects_cpu_tensors_in_native_op():
+    q, k = _qk()
+    with pytest.raises(RuntimeError, match="CUDA tensors"):
+        build_plan(q, k, sample_pages=2)
+
+
+def test_native_op_checks():
+    q, k = _qk()
+    with pytest.raises(RuntimeError, match="CUDA"):
+        _C.ibcs(q, k)
+    s = torch.zeros(4, 16)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        _C.sip(s, torch.zeros(4), torch.zeros(4, 2, dtype=torch.int32), torch.zeros(4, 2))
+
+
+def test_paged_attention_value_errors():
+    q = torch.zeros(1, 2, 512, 128, dtype=torch.bfloat16)
+    rows = 2 * 4
+    desc = torch.zeros(rows, 1, 32, dtype=torch.int32)
+    w = torch.zeros(rows, 1, 32)
+    with pytest.raises(ValueError, match="same"):
+        paged_attention(q, q[:, :1], q, desc, w)
+    with pytest.raises(ValueError, match="GPU"):
+        paged_attention(q, q, q, desc, w)
+
+
+
+def test_apply_plan_forwards_validation():
+    q = torch.zeros(1, 1, 256, 128, dtype=torch.bfloat16)
+    plan = SamplePlan(torch.zeros(3, 1, 32, dtype=torch.int32), torch.zeros(3, 1, 32))
+    with pytest.raises(ValueError):
+        apply_plan(q, q, q, plan)
+
+
+def test_heads_per_chunk_budget():
+    from ab_attention.attention import _heads_per_chunk
+
+    # Wan2.1-14B 720p runs as one chunk within the 16 GiB budget
+    assert _heads_per_chunk(80, 591, 75600) == 80
+    assert _heads_per_chunk(4, 10, 1280) == 4

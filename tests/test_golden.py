@@ -1,0 +1,79 @@
+"""The committed c0 fixture (tests/golden/c0_head0.npz, written by
+tests/golden/make_golden.py): the CPU oracle reproduces it bit for bit, and on
+the GPU the HIP library matches it stage by stage (bit-exact where the
+algorithm allows, within tolerance where the reference itself is approximate)."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+FIX = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "c0_head0.npz")
+
+
+@pytest.fixture(scope="module")
+def fx():
+    return dict(np.load(FIX, allow_pickle=False))
+
+
+def test_oracle_reproduces_fixture(oracle_mod, fx):
+    n = fx["q"].shape[1]
+    cent, pops = oracle_mod.cluster(fx["q"], 1, n)
+    np.testing.assert_array_equal(cent, fx["centroids"])
+    np.testing.assert_array_equal(pops, fx["populations"])
+    pooled = oracle_mod.pool(fx["k"], 1, n)
+    np.testing.assert_array_equal(pooled, fx["pooled"])
+    lse, mx, den = oracle_mod.lse(cent, pooled, 1, n)
+    np.testing.assert_array_equal(lse, fx["lse"])
+    np.testing.assert_array_equal(mx, fx["lse_max"])
+    np.testing.assert_array_equal(den, fx["lse_den"])
+    scores = oracle_mod.masses(lse, pops, mx, den, cent.shape[0], n // 4)
+    np.testing.assert_array_equal(scores, fx["scores"])
+    ids, logw = oracle_mod.sip(scores, fx["offsets"], int(fx["sample_pages"]) * 32)
+    np.testing.assert_array_equal(ids, fx["ids"])
+    np.testing.assert_array_equal(logw.view(np.uint32), fx["log_weights"].view(np.uint32))
+    f32 = lambda b: oracle_mod.bits_to_f32(b).reshape(1, n, 128)
+    out, lse2 = oracle_mod.prefill(f32(fx["q"]), f32(fx["k"]), f32(fx["v"]), ids, logw)
+    np.testing.assert_array_equal(out, fx["out"])
+    np.testing.assert_array_equal(lse2, fx["out_lse"])
+
+
+def _dev(bits):
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).cuda()
+
+
+@pytest.mark.gpu
+def test_gpu_matches_fixture(native, fx):
+    from ab_attention import _C, _lib
+    from ab_attention.flashinfer_backend import paged_attention
+
+    n = fx["q"].shape[1]
+    rows, fb = fx["scores"].shape
+    q, k, v = (_dev(fx[t]).reshape(1, 1, n, 128) for t in ("q", "k", "v"))
+    cent = torch.empty((rows, 8, 128), dtype=torch.bfloat16, device="cuda")
+    pops = torch.empty((rows, 8), device="cuda")
+    pooled = torch.empty((1, fb, 2, 128), dtype=torch.bfloat16, device="cuda")
+    _lib.check(native.ab_ibcs_cluster_pool(_lib.ptr(q), _lib.ptr(k), 1, n, _lib.ptr(cent), _lib.ptr(pops),
+                                           _lib.ptr(pooled), _lib.stream(q.device)))
+    torch.cuda.synchronize()
+    bits = lambda t: t.cpu().view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(bits(cent).reshape(fx["centroids"].shape), fx["centroids"])
+    np.testing.assert_array_equal(pops.cpu().numpy(), fx["populations"])
+    np.testing.assert_array_equal(bits(pooled).reshape(fx["pooled"].shape), fx["pooled"])
+    scores = _C.ibcs(q, k).cpu().numpy()
+    np.testing.assert_allclose(scores, fx["scores"], rtol=3e-2, atol=1e-9)
+    assert np.median(np.abs(scores - fx["scores"]) / fx["scores"]) < 1e-6
+    # SIP on the fixture's masses: bit-exact
+    ids = torch.empty_like(torch.from_numpy(fx["ids"])).cuda()
+    logw = torch.empty_like(torch.from_numpy(fx["log_weights"])).cuda()
+    _C.sip(torch.from_numpy(fx["scores"]).cuda(), torch.from_numpy(fx["offsets"]).cuda(), ids, logw)
+    np.testing.assert_array_equal(ids.cpu().numpy(), fx["ids"])
+    np.testing.assert_array_equal(logw.cpu().numpy().view(np.uint32), fx["log_weights"].view(np.uint32))
+    # prefill on the fixture's plan: bf16 tolerance
+    pages = int(fx["sample_pages"])
+    out, lse = paged_attention(q, k, v, ids.reshape(rows, pages, 32), logw.reshape(rows, pages, 32),
+                               return_lse=True)
+    got = out.float().cpu().numpy().reshape(1, n, 128)
+    assert np.abs(got - fx["out"]).max() <= 2e-2
+    assert np.linalg.norm(got - fx["out"]) / np.linalg.norm(fx["out"]) <= 1e-2
+    assert np.abs(lse.cpu().numpy().reshape(1, n) - fx["out_lse"]).max() <= 1e-3
