@@ -4,7 +4,7 @@
 // Dataflow (one head chunk, the caller's workspace holds every intermediate):
 //   cluster_pool_kernel  Q,K -> scaled centroids [rows,8,128] bf16, populations
 //                        [rows,8] f32, pooled keys [bh,fb,2,128] bf16
-//   lse_kernel           centroids x pooled keys (bf16 MFMA) -> fp16 pair-LSE
+//   (lse.hip)            centroids x pooled keys (bf16 MFMA) -> fp16 pair-LSE
 //                        [rows,8,ld] and (max, den) [rows,8]
 //   masses_kernel        pair-LSE + normalisers + populations -> scores [rows,fb]
 //
@@ -212,182 +212,6 @@ __global__ __launch_bounds__(kClusterThreads) void cluster_pool_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Stage 3: pair-LSE of every (centroid, KV4 block) with online normalisers.
-//
-// One workgroup = 4 waves = 8 query blocks (64 centroid rows) of one head; it
-// streams all of the head's pooled keys through LDS in tiles of 64 KV4 blocks
-// (128 pooled rows, 32 KiB, double buffered). Each wave computes a 16 x 64
-// tile per rep with v_mfma_f32_16x16x32_bf16: A = its 16 centroid rows (kept
-// in registers), B = pooled rows. MFMA column c of n-tile nt is KV4 block
-// 4c + nt, so a lane holds 4 consecutive blocks per centroid row and stores
-// them as one 8-byte fp16 vector.
-
-constexpr int kLseThreads = 256;
-constexpr int kLseQBlocks = 8;            // query blocks per workgroup
-constexpr int kLseTileBlocks = 64;        // KV4 blocks per LDS tile
-constexpr int kLseTileRows = kLseTileBlocks * kReps;
-constexpr int kLseStageBytes = kLseTileRows * kHeadDim * 2;  // 32 KiB
-
-__device__ __forceinline__ int lse_swizzle(int row, int chunk) {
-    return row * 16 + (chunk ^ ((row >> 3) & 15));
-}
-
-__device__ __forceinline__ void combine_pair(float& m, float& d, float om, float od) {
-    const float nm = fmaxf(m, om);
-    d = d * fast_exp2(m - nm) + od * fast_exp2(om - nm);
-    m = nm;
-}
-
-__global__ __launch_bounds__(kLseThreads, 2) void lse_kernel(
-    const uint16_t* __restrict__ centroids, const uint16_t* __restrict__ pooled,
-    _Float16* __restrict__ lse, float* __restrict__ lse_max, float* __restrict__ lse_den,
-    int64_t qb, int fb, int64_t ld, int groups_per_head, int total_groups) {
-    extern __shared__ __align__(16) unsigned char smem[];
-    auto stage = [&](int i) { return reinterpret_cast<u32x4*>(smem + i * kLseStageBytes); };
-
-    // XCD-aware order: hardware deals workgroups round-robin over 8 XCDs, so
-    // consecutive logical groups (same head) are given to one XCD.
-    const int hw = blockIdx.x;
-    const int per_xcd = (total_groups + 7) / 8;
-    const int logical = (hw & 7) * per_xcd + (hw >> 3);
-    if (logical >= total_groups) return;
-    const int64_t bh = logical / groups_per_head;
-    const int64_t qgroup = logical % groups_per_head;
-
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int col = lane & 15, quad = lane >> 4;
-
-    // A operand: centroid row (wave*16 + col), dims 32s + 8*quad .. +8.
-    const int64_t qblock0 = qgroup * kLseQBlocks + wave * 2;
-    bf16x8 a_op[4];
-    {
-        const int64_t qbk = qblock0 + (col >> 3);
-        const int cent = col & 7;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            u32x4 v = {0u, 0u, 0u, 0u};
-            if (qbk < qb)
-                v = *reinterpret_cast<const u32x4*>(
-                    centroids + ((bh * qb + qbk) * kCentroids + cent) * kHeadDim + 32 * s + 8 * quad);
-            a_op[s] = __builtin_bit_cast(bf16x8, v);
-        }
-    }
-
-    const u32x4* head_keys = reinterpret_cast<const u32x4*>(pooled + bh * int64_t(fb) * kReps * kHeadDim);
-    const int tiles = (fb + kLseTileBlocks - 1) / kLseTileBlocks;
-
-    auto load_tile = [&](int tile, u32x4 (&regs)[8]) {
-#pragma unroll
-        for (int p = 0; p < 8; ++p) {
-            const int idx = p * kLseThreads + tid;  // 16-byte chunk within the tile
-            const int r = idx >> 4;
-            const int blockj = tile * kLseTileBlocks + (r >> 1);
-            u32x4 v = {0u, 0u, 0u, 0u};
-            if (blockj < fb) v = head_keys[int64_t(tile) * kLseTileRows * 16 + idx];
-            regs[p] = v;
-        }
-    };
-    auto store_tile = [&](u32x4* dst, const u32x4 (&regs)[8]) {
-#pragma unroll
-        for (int p = 0; p < 8; ++p) {
-            const int idx = p * kLseThreads + tid;
-            dst[lse_swizzle(idx >> 4, idx & 15)] = regs[p];
-        }
-    };
-
-    // Output rows owned by this lane: centroid rows quad*4 + v of the wave.
-    const int64_t my_qblock = qblock0 + (quad >> 1);
-    const bool row_ok = my_qblock < qb;
-    const int cent0 = (quad & 1) * 4;
-    _Float16* out_row = lse + ((bh * qb + my_qblock) * kCentroids + cent0) * ld;
-
-    float run_max[4], run_den[4];
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-        run_max[v] = -FLT_MAX;
-        run_den[v] = 0.0f;
-    }
-
-    u32x4 regs[8];
-    load_tile(0, regs);
-    store_tile(stage(0), regs);
-    __syncthreads();
-
-    for (int tile = 0; tile < tiles; ++tile) {
-        const bool more = tile + 1 < tiles;
-        if (more) load_tile(tile + 1, regs);
-        const u32x4* cur = stage(tile & 1);
-
-        f32x4 acc[4][2];
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt) {
-#pragma unroll
-            for (int r = 0; r < 2; ++r) {
-                const int prow = 2 * (4 * col + nt) + r;
-                f32x4 c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int s = 0; s < 4; ++s) {
-                    const bf16x8 b = __builtin_bit_cast(bf16x8, cur[lse_swizzle(prow, 4 * s + quad)]);
-                    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_op[s], b, c, 0, 0, 0);
-                }
-                acc[nt][r] = c;
-            }
-        }
-
-        // Epilogue: lane holds centroid rows quad*4+v, blocks 4*col + nt.
-        const int jbase = tile * kLseTileBlocks + 4 * col;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            float f[4];
-            _Float16 h[4];
-#pragma unroll
-            for (int nt = 0; nt < 4; ++nt) {
-                const float a = acc[nt][0][v] + 1.0f;
-                const float b = acc[nt][1][v] + 1.0f;
-                const float mx = fmaxf(a, b), mn = fminf(a, b);
-                const float l = mx + fast_log2(1.0f + fast_exp2(mn - mx));
-                h[nt] = static_cast<_Float16>(l);
-                f[nt] = (jbase + nt < fb) ? static_cast<float>(h[nt]) : -INFINITY;
-            }
-            if (row_ok && jbase < fb) {
-                typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-                const f16x4 packed = {h[0], h[1], h[2], h[3]};
-                *reinterpret_cast<f16x4*>(out_row + int64_t(v) * ld + jbase) = packed;
-            }
-            const float tmax = fmaxf(fmaxf(f[0], f[1]), fmaxf(f[2], f[3]));
-            const float nm = fmaxf(run_max[v], tmax);
-            float d = run_den[v] * fast_exp2(run_max[v] - nm);
-#pragma unroll
-            for (int nt = 0; nt < 4; ++nt) d += fast_exp2(f[nt] - nm);
-            run_den[v] = d;
-            run_max[v] = nm;
-        }
-
-        if (more) store_tile(stage((tile + 1) & 1), regs);
-        __syncthreads();
-    }
-
-    // Merge the 16 lanes (columns) that share each centroid row.
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const float om = __shfl_xor(run_max[v], off);
-            const float od = __shfl_xor(run_den[v], off);
-            combine_pair(run_max[v], run_den[v], om, od);
-        }
-    }
-    if (col == 0 && row_ok) {
-        const int64_t slot = (bh * qb + my_qblock) * kCentroids + cent0;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            lse_max[slot + v] = run_max[v];
-            lse_den[slot + v] = run_den[v];
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
 // Stage 4: population-weighted masses, one workgroup per row:
 //   m_j = sum_s fmaf(n_s, exp2(l_sj - M_s) * (1/D_s), .) * (1 / sum_s n_s).
 
@@ -446,28 +270,6 @@ int launch_cluster_pool(const void* q, const void* k, int64_t bh, int64_t n, voi
                        static_cast<uint16_t*>(centroids), pops, static_cast<uint16_t*>(pooled), n, qb,
                        qk_scale_log2);
     return check_launch("cluster_pool_kernel");
-}
-
-int launch_lse(const void* centroids, const void* pooled, int64_t bh, int64_t n, void* lse,
-               float* lse_max, float* lse_den, hipStream_t stream) {
-    const int64_t qb = (n + kQueryBlock - 1) / kQueryBlock;
-    const int64_t fb = n / kKvBlock;
-    const int groups_per_head = static_cast<int>((qb + kLseQBlocks - 1) / kLseQBlocks);
-    const int64_t total = groups_per_head * bh;
-    if (total > (int64_t(1) << 30)) return set_error(1, "ibcs: too many query blocks (%lld)", (long long)total);
-    const int per_xcd = static_cast<int>((total + 7) / 8);
-    const size_t lds = 2 * kLseStageBytes;
-    static bool attr_set = false;
-    if (!attr_set) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(lse_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-        attr_set = true;
-    }
-    hipLaunchKernelGGL(lse_kernel, dim3(static_cast<unsigned>(per_xcd * 8)), dim3(kLseThreads), lds, stream,
-                       static_cast<const uint16_t*>(centroids), static_cast<const uint16_t*>(pooled),
-                       static_cast<_Float16*>(lse), lse_max, lse_den, qb, static_cast<int>(fb),
-                       lse_stride(fb), groups_per_head, static_cast<int>(total));
-    return check_launch("lse_kernel");
 }
 
 int launch_masses(const void* lse, const float* pops, const float* lse_max, const float* lse_den,

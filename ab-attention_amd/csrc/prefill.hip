@@ -8,19 +8,25 @@
 // (ab_attention/flashinfer_backend.py:30-59): logits + w / (sm_scale*log2 e),
 // then an online softmax in base 2 with scale sm_scale*log2 e.
 //
-// Kernel shape: one workgroup (4 waves) per row; wave w owns queries
-// 32w..32w+31. The row's pages are streamed in tiles of 16 KV4 blocks (64
-// keys): each tile's K rows and transposed V are staged in LDS (double
-// buffered, global loads of tile t+1 in flight while tile t computes).
+// Kernel shape: one workgroup (4 waves) per row, two workgroups per CU; wave
+// w owns queries 32w..32w+31. The row's pages are streamed in tiles of 8 KV4
+// blocks (32 keys) through a ring of kStages LDS stages that the hardware
+// fills directly from global memory (global_load_lds_dwordx4: no staging
+// registers, kStages-1 tiles in flight per workgroup). Each wave moves one
+// quarter of every tile and waits only for its own tile-t transfers
+// (s_waitcnt vmcnt) before the workgroup barrier that publishes tile t.
+// The page ids and weights of the row reach LDS the same way, 64 tiles at a
+// time, so the loop issues no other global or scalar loads.
 //   S^T = K Q^T  : v_mfma_f32_32x32x16_bf16, A = K rows from LDS, B = Q in VGPRs
-//                  -> each lane holds one query and 16 keys per 32-key half,
-//                     in 4-key groups that are exactly one KV4 block.
+//                  -> each lane holds one query and 16 keys, in 4-key groups
+//                     that are exactly one KV4 block.
 //   O^T += V^T P^T: A = V^T read from the row-major V tile with the
 //                  transposing LDS read ds_read_b64_tr_b16, B = P straight
 //                  from the S^T accumulators (bf16); the key order of each
 //                  MFMA k-step is chosen so no cross-lane movement is needed.
-// LDS tiles (16 KiB each, double buffered) are swizzled so that both the
-// 16-byte stores from the loader and the operand reads are bank-conflict free:
+// LDS tiles are swizzled so that the operand reads are bank-conflict free. A
+// transfer instruction writes 1 KiB contiguously (lane j at +16j), so the
+// swizzle is realised by the choice of each lane's source address:
 //   K: [key][16 chunks of 16 B], chunk position = chunk ^ (key & 15);
 //   V: per page 8 blocks of 4 keys x 16 dims (128 B); inside block m the row
 //      of key r sits at position r ^ ((m >> 1) & 3), so each 16-lane group of
@@ -31,15 +37,25 @@ namespace ab {
 namespace {
 
 constexpr int kPfThreads = 256;
-constexpr int kTilePages = 16;
-constexpr int kTileKeys = kTilePages * kKvBlock;              // 64
-constexpr int kTileBytes = kTileKeys * kHeadDim * 2;         // 16 KiB
-constexpr int kStageBytes = 2 * kTileBytes + 128;             // K, V, weights
+constexpr int kStages = 4;
+constexpr int kTilePages = 8;                                  // KV4 blocks per tile
+constexpr int kPageBytes = kKvBlock * kHeadDim * 2;            // 1 KiB of K (or V)
+constexpr int kHalfBytes = kTilePages * kPageBytes;            // K (or V) of one tile
+constexpr int kStageBytes = 2 * kHalfBytes;                    // 16 KiB
+constexpr int kBatchTiles = 64;                                // ids/weights per LDS batch
+constexpr int kBatchBytes = kBatchTiles * kTilePages * 4;      // 2 KiB
+constexpr int kIdsOffset = kStages * kStageBytes;              // 2 batch buffers of ids
+constexpr int kWeightsOffset = kIdsOffset + 2 * kBatchBytes;   // 2 batch buffers of weights
+constexpr int kLdsBytes = kWeightsOffset + 2 * kBatchBytes;
+constexpr int kDmaPerTile = 4;                                 // transfers per wave per tile
 // Largest p = 2^(y) allowed before the running reference is moved.
 constexpr float kSlack = 8.0f;
 
+static_assert(kLdsBytes * 2 <= 160 * 1024, "two workgroups per CU must fit in LDS");
+
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+typedef __attribute__((address_space(3))) unsigned char lds_u8;
 
 // Transposing LDS read: within each 16-lane group, lane i receives element
 // i%4 of the 8 bytes read by lanes 4r + i/4, for r = 0..3 (so the group reads
@@ -47,6 +63,27 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 // gets one column).
 __device__ __forceinline__ i16x4 lds_read_tr16(const unsigned char* p) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+}
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// 16 bytes per lane from base + voffset straight into LDS: lane j writes LDS
+// bytes [lds + 16j, lds + 16j + 16). The transfer is counted by vmcnt. The
+// kernel holds nothing in m0 across these statements.
+__device__ __forceinline__ void dma16(const void* base, uint32_t voffset, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voffset), "s"(base)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// s_waitcnt with vmcnt(N) and lgkmcnt(0) (expcnt left open), then a workgroup
+// barrier that the compiler cannot move memory accesses across.
+template <int N>
+__device__ __forceinline__ void wait_and_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+    asm volatile("s_barrier" ::: "memory");
 }
 
 __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
@@ -68,10 +105,12 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
     if (bh >= rows / qb || blk >= qb) return;
     const int64_t row = bh * qb + blk;
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int qi = lane & 31, half = lane >> 5;
     const int64_t token = blk * kQueryBlock + wave * 32 + qi;
     const bool valid_q = token < n;
+    const int tiles = samples / kTilePages;
 
     // Q as the B operand of S^T = K Q^T: dims 16s + 8*half .. +8.
     bf16x8 bq[8];
@@ -85,54 +124,64 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
         }
     }
 
+    const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)smem));
     const int32_t* row_ids = ids + row * int64_t(samples);
     const float* row_w = logw + row * int64_t(samples);
-    const u32x4* kbase = reinterpret_cast<const u32x4*>(k + bh * n * kHeadDim);
-    const u32x4* vbase = reinterpret_cast<const u32x4*>(v + bh * n * kHeadDim);
-    const int tiles = samples / kTilePages;
+    const uint16_t* kbase = k + bh * n * kHeadDim;
+    const uint16_t* vbase = v + bh * n * kHeadDim;
 
-    // Loader role: page lp = tid/16 of the tile, 16-byte chunk lc = tid%16.
-    const int lp = tid >> 4, lc = tid & 15;
-    u32x4 kreg[4], vreg[4];
-    float wreg = 0.f;
-    auto load_tile = [&](int tile) {
-        // Clamp so a malformed plan can never address outside the head.
-        const int64_t j = min(max(row_ids[tile * kTilePages + lp], 0), fb - 1);
-        const int64_t first = (4 * j) * 16 + lc;  // in 16-byte units
+    // Batch b of ids and weights (tiles 64b .. 64b+63) into buffer b & 1, by
+    // wave 0: two 1 KiB transfers each. Lanes past the row's end re-read its
+    // last 16 bytes (those entries are never used).
+    const uint32_t row_bytes = static_cast<uint32_t>(samples) * 4u;
+    auto issue_batch = [&](int b) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            kreg[i] = kbase[first + 16 * i];
-            vreg[i] = vbase[first + 16 * i];
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t src = min(uint32_t(b) * kBatchBytes + i * 1024u + 16u * lane, row_bytes - 16u);
+            const uint32_t dst = (b & 1) * kBatchBytes + i * 1024u;
+            dma16(row_ids, src, lds0 + kIdsOffset + dst);
+            dma16(row_w, src, lds0 + kWeightsOffset + dst);
         }
-        wreg = row_w[tile * kTilePages + lp];
     };
-    // Loader's LDS offsets (key 4*lp + i, 16-byte chunk lc).
-    const int v_store = lp * 1024 + (lc >> 1) * 128 + (lc & 1) * 16;
-    const int v_swz = (lc >> 2) & 3;  // (block >> 1) & 3 with block = lc >> 1
-    auto store_tile = [&](unsigned char* st) {
+
+    // Tile transfers of this wave: pages 2w and 2w+1 of the tile, K and V.
+    // Source offsets inside a page (1 KiB = 4 keys x 256 B) for lane j:
+    //   K: key r = j/16 at LDS chunk position j%16 holds chunk pos ^ (key & 15);
+    //   V: block m = j/8, row slot (j/2)%4 holds key slot ^ ((m>>1)&3), dims 16m + 8(j%2).
+    uint32_t k_src[2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int key = 4 * lp + i;
-            *reinterpret_cast<u32x4*>(st + key * 256 + 16 * (lc ^ (key & 15))) = kreg[i];
-            *reinterpret_cast<u32x4*>(st + kTileBytes + v_store + 32 * (i ^ v_swz)) = vreg[i];
-        }
-        if (lc == 0) {
-            // weights ordered [half][kt][g] for page 8kt + 2g + half
-            const int h = lp & 1, kt = lp >> 3, g = (lp >> 1) & 3;
-            reinterpret_cast<float*>(st + 2 * kTileBytes)[h * 8 + kt * 4 + g] = wreg;
-        }
+    for (int e = 0; e < 2; ++e) {
+        const int r = lane >> 4, pos = lane & 15;
+        const int key = 4 * (2 * wave + e) + r;
+        k_src[e] = uint32_t(r * 16 + (pos ^ (key & 15))) * 16u;
+    }
+    const uint32_t v_src = [&] {
+        const int m = lane >> 3, sl = (lane >> 1) & 3, h = lane & 1;
+        return uint32_t((sl ^ ((m >> 1) & 3)) * 16 + 2 * m + h) * 16u;
+    }();
+    auto issue_tile = [&](int u) {
+        const int* idp = reinterpret_cast<const int*>(smem + kIdsOffset + ((u / kBatchTiles) & 1) * kBatchBytes) +
+                         (u % kBatchTiles) * kTilePages + 2 * wave;
+        // Clamp so a malformed plan can never address outside the head.
+        const uint32_t j0 = uint32_t(min(max(idp[0], 0), fb - 1));
+        const uint32_t j1 = uint32_t(min(max(idp[1], 0), fb - 1));
+        const uint32_t st = lds0 + (u % kStages) * kStageBytes + 2 * wave * kPageBytes;
+        dma16(kbase, j0 * kPageBytes + k_src[0], st);
+        dma16(kbase, j1 * kPageBytes + k_src[1], st + kPageBytes);
+        dma16(vbase, j0 * kPageBytes + v_src, st + kHalfBytes);
+        dma16(vbase, j1 * kPageBytes + v_src, st + kHalfBytes + kPageBytes);
     };
 
     // Operand-read offsets of this lane (stage-relative).
-    int k_off[8];  // S^T A operand: key qi (+32kt), chunk 2s + half
+    int k_off[8];  // S^T A operand: key qi, chunk 2s + half
 #pragma unroll
     for (int s8 = 0; s8 < 8; ++s8) k_off[s8] = qi * 256 + 16 * ((2 * s8 + half) ^ (qi & 15));
     int v_off[4];  // PV A operand, transposing read: page half (+4ks + 2t), block 2dt + (lane>>4)&1
     {
-        const int gd = (lane >> 4) & 1, r = (lane >> 2) & 3, q = lane & 3;
+        const int gd = (lane >> 4) & 1, r = (lane >> 2) & 3, q4 = lane & 3;
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt)
-            v_off[dt] = kTileBytes + half * 1024 + (2 * dt + gd) * 128 + 32 * (r ^ dt) + 8 * q;
+            v_off[dt] = kHalfBytes + half * 1024 + (2 * dt + gd) * 128 + 32 * (r ^ dt) + 8 * q4;
     }
 
     f32x16 o_acc[4];
@@ -142,48 +191,56 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
         for (int r = 0; r < 16; ++r) o_acc[dt][r] = 0.f;
     float m_run = 0.f, l_run = 0.f;  // reference set by the first tile
 
-    load_tile(0);
-    store_tile(smem);
-    __syncthreads();
+    // Prologue: the first batch of ids/weights (this also completes the Q
+    // loads), then tiles 0 .. kStages-2.
+    if (wave == 0) issue_batch(0);
+    wait_and_barrier<0>();
+    for (int u = 0; u < kStages - 1 && u < tiles; ++u) issue_tile(u);
 
     for (int tile = 0; tile < tiles; ++tile) {
-        const bool more = tile + 1 < tiles;
-        if (more) load_tile(tile + 1);
-        const unsigned char* st = smem + (tile & 1) * kStageBytes;
-        const float* ws = reinterpret_cast<const float*>(st + 2 * kTileBytes);
+        // This wave's transfers for tile t are done once at most 4g newer ones
+        // (tiles t+1 .. t+g) are outstanding; the barrier then publishes the
+        // whole tile and retires every read of the stage refilled below.
+        const int ahead = tiles - 1 - tile;
+        if (ahead >= kStages - 2)
+            wait_and_barrier<kDmaPerTile * (kStages - 2)>();
+        else if (ahead == 1)
+            wait_and_barrier<kDmaPerTile>();
+        else
+            wait_and_barrier<0>();
+        if (tile + kStages - 1 < tiles) issue_tile(tile + kStages - 1);
+        if (wave == 0 && tile % kBatchTiles == kBatchTiles / 2 && (tile / kBatchTiles + 1) * kBatchTiles < tiles)
+            issue_batch(tile / kBatchTiles + 1);
 
-        // S^T for the two 32-key halves.
-        f32x16 sacc[2];
+        const unsigned char* st = smem + (tile % kStages) * kStageBytes;
+        const float* ws = reinterpret_cast<const float*>(smem + kWeightsOffset +
+                                                         ((tile / kBatchTiles) & 1) * kBatchBytes) +
+                          (tile % kBatchTiles) * kTilePages;
+
+        // S^T of the tile's 32 keys.
+        f32x16 sacc;
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-            f32x16 c;
+        for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) c[r] = 0.f;
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                const bf16x8 a = __builtin_bit_cast(
-                    bf16x8, *reinterpret_cast<const u32x4*>(st + k_off[s] + kt * 32 * 256));
-                c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bq[s], c, 0, 0, 0);
-            }
-            sacc[kt] = c;
+        for (int s = 0; s < 8; ++s) {
+            const bf16x8 a = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(st + k_off[s]));
+            sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bq[s], sacc, 0, 0, 0);
         }
 
         // Logits in base 2 with the block weights; lane register r holds key
-        // 8*(r/4) + 4*half + r%4 of its half, i.e. page 8kt + 2(r/4) + half.
+        // 8*(r/4) + 4*half + r%4 of the tile, i.e. page 2(r/4) + half.
         // Scores are kept relative to the running reference m_run:
         //   y = s * log2(e)/sqrt(d) + (w - m_run),   p = 2^y.
-        float wm[8];
+        float wm[4];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) wm[i] = ws[half * 8 + i] - m_run;
+        for (int g = 0; g < 4; ++g) wm[g] = ws[2 * g + half] - m_run;
         float tmax = -INFINITY;
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float y = __builtin_fmaf(sacc[kt][r], scale_log2, wm[kt * 4 + (r >> 2)]);
-                sacc[kt][r] = y;
-                tmax = fmaxf(tmax, y);
-            }
+        for (int r = 0; r < 16; ++r) {
+            const float y = __builtin_fmaf(sacc[r], scale_log2, wm[r >> 2]);
+            sacc[r] = y;
+            tmax = fmaxf(tmax, y);
+        }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
         // Lazy rescaling: the reference moves only when the tile maximum exceeds
         // it by more than kSlack (so p <= 2^kSlack); the branch is wave-uniform.
@@ -198,49 +255,41 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
 #pragma unroll
                 for (int r = 0; r < 16; ++r) o_acc[dt][r] *= alpha;
 #pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) sacc[kt][r] -= shift;
+            for (int r = 0; r < 16; ++r) sacc[r] -= shift;
         }
         float psum = 0.f;
-        uint32_t pw[2][4][2];
+        uint32_t pw[4][2];
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
+        for (int g = 0; g < 4; ++g) {
+            float p[4];
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                float p[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    p[i] = fast_exp2(sacc[kt][4 * g + i]);
-                    psum += p[i];
-                }
-                pw[kt][g][0] = pack_bf16(p[0], p[1]);
-                pw[kt][g][1] = pack_bf16(p[2], p[3]);
+            for (int i = 0; i < 4; ++i) {
+                p[i] = fast_exp2(sacc[4 * g + i]);
+                psum += p[i];
             }
+            pw[g][0] = pack_bf16(p[0], p[1]);
+            pw[g][1] = pack_bf16(p[2], p[3]);
+        }
         l_run += psum;
 
-        // O^T += V^T P^T over 4 k-steps of 16 keys. MFMA k-index 8*half + 4t + r
+        // O^T += V^T P^T over 2 k-steps of 16 keys. MFMA k-index 8*half + 4t + r
         // of k-step ks is key r of tile page 4*ks + 2t + half, on both operands.
         // A operand of lane (group g = lane/16, i = lane%16): two transposing
         // reads; the source lane 4r + q addresses key r of that page, dims
         // 32dt + 16(g%2) + 4q .. +3, so lane i receives dim 32dt + 16(g%2) + i.
 #pragma unroll
-        for (int ks4 = 0; ks4 < 4; ++ks4) {
-            const int kt = ks4 >> 1, g0 = 2 * (ks4 & 1);
-            const u32x4 bw = {pw[kt][g0][0], pw[kt][g0][1], pw[kt][g0 + 1][0], pw[kt][g0 + 1][1]};
+        for (int ks = 0; ks < 2; ++ks) {
+            const u32x4 bw = {pw[2 * ks][0], pw[2 * ks][1], pw[2 * ks + 1][0], pw[2 * ks + 1][1]};
             const bf16x8 b = __builtin_bit_cast(bf16x8, bw);
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) {
-                const unsigned char* p0 = st + v_off[dt] + ks4 * 4096;
+                const unsigned char* p0 = st + v_off[dt] + ks * 4096;
                 const i16x4 lo = lds_read_tr16(p0);
                 const i16x4 hi = lds_read_tr16(p0 + 2048);
                 const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
                 o_acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, o_acc[dt], 0, 0, 0);
             }
         }
-
-        if (more) store_tile(smem + ((tile + 1) & 1) * kStageBytes);
-        __syncthreads();
     }
 
     const float l_tot = l_run + __shfl_xor(l_run, 32);
@@ -267,18 +316,21 @@ int launch_prefill(const void* q, const void* k, const void* v, int64_t bh, int6
     const int64_t rows = bh * qb;
     if (samples % kTilePages != 0)
         return set_error(1, "prefill: samples (%lld) must be a multiple of %d", (long long)samples, kTilePages);
+    if ((reinterpret_cast<uintptr_t>(ids) & 15u) || (reinterpret_cast<uintptr_t>(logw) & 15u))
+        return set_error(1, "prefill: ids and log_weights must be 16-byte aligned");
+    if (n * kHeadDim * 2 > int64_t(0xffffffff))
+        return set_error(1, "prefill: one head of K/V must be under 4 GiB");
     const float scale_log2 = static_cast<float>(1.4426950408889634 / 11.313708498984761);  // log2(e)/sqrt(128)
     const int64_t per_xcd = (qb + 7) / 8;
-    const size_t lds = 2 * kStageBytes;
     static bool attr_set = false;
     if (!attr_set) {
         (void)hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
         attr_set = true;
     }
     if (rows == 0) return 0;
-    hipLaunchKernelGGL(prefill_kernel, dim3(static_cast<unsigned>(per_xcd * 8 * bh)), dim3(kPfThreads), lds, stream,
-                       static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+    hipLaunchKernelGGL(prefill_kernel, dim3(static_cast<unsigned>(per_xcd * 8 * bh)), dim3(kPfThreads), kLdsBytes,
+                       stream, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                        static_cast<const uint16_t*>(v), ids, logw, static_cast<uint16_t*>(out), lse, n, qb, rows,
                        static_cast<int>(n / kKvBlock), static_cast<int>(samples), scale_log2);
     return check_launch("prefill_kernel");

@@ -79,6 +79,20 @@ def test_prefill_random_plan_with_duplicates(oracle_mod):
     _check(q, k, v, ids, logw, oracle_mod)
 
 
+def test_prefill_partial_id_batch(oracle_mod):
+    """640 sampled blocks (80 tiles of 8): the kernel's second batch of page ids
+    and weights is partial, so its tail is read clamped to the row's end."""
+    rng = np.random.default_rng(12)
+    torch.manual_seed(3)
+    n = 4096
+    q, k, v = (torch.randn(1, 1, n, 128).to(torch.bfloat16) for _ in range(3))
+    print("prefill n=4096 samples=640", flush=True)
+    rows, fb = n // 128, n // 4
+    ids = np.sort(rng.choice(fb, size=(rows, 640), replace=True), axis=1).astype(np.int32)
+    logw = (rng.random((rows, 640)) * 5).astype(np.float32)
+    _check(q, k, v, ids, logw, oracle_mod)
+
+
 def test_prefill_c1_head_subset(oracle_mod):
     """One Wan2.1-1.3B head at full length (32,760 tokens, partial last block),
     64 sample pages; the oracle checks the first and last three rows."""
