@@ -94,10 +94,7 @@ __global__ __launch_bounds__(kClusterThreads) void cluster_pool_kernel(
     __shared__ float center_row[kHeadDim];
     __shared__ float s_val[2];
     __shared__ int s_idx[2];
-    __shared__ int assignment[kQueryBlock];
-    __shared__ int members[kQueryBlock];
-    __shared__ int counts[kCentroids];
-    __shared__ int starts[kCentroids];
+    __shared__ uint64_t slot_mask[kClusterThreads / 64][kCentroids];
 
     const int tid = threadIdx.x;
     const int64_t blk = blockIdx.x, bh = blockIdx.y;
@@ -122,7 +119,15 @@ __global__ __launch_bounds__(kClusterThreads) void cluster_pool_kernel(
     // Per-dim mean over valid queries in row order (csrc/ibcs.cu:130-140).
     {
         float sum = 0.0f;
-        for (int i = 0; i < valid; ++i) sum += block_elem(block, i, tid);
+        int i = 0;
+        for (; i + 8 <= valid; i += 8) {  // 8 reads in flight, adds in row order
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = block_elem(block, i + e, tid);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sum += v[e];
+        }
+        for (; i < valid; ++i) sum += block_elem(block, i, tid);
         center_row[tid] = __fdiv_rn(sum, static_cast<float>(valid));
     }
     float x[kHeadDim];
@@ -154,39 +159,50 @@ __global__ __launch_bounds__(kClusterThreads) void cluster_pool_kernel(
         __syncthreads();
     }
 
-    // Populations and a slot-major member list that keeps query order.
-    assignment[tid] = live ? assign : -1;
-    __syncthreads();
-    if (tid < kCentroids) {
-        int c = 0;
-        for (int i = 0; i < valid; ++i) c += assignment[i] == tid;
-        counts[tid] = c;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        int s = 0;
-        for (int c = 0; c < kCentroids; ++c) {
-            starts[c] = s;
-            s += counts[c];
+    // Members of each slot: per wave, the ballot of the queries assigned to
+    // it. Queries 64w + bit, walked wave by wave and bit by bit, come in
+    // query order (the reference's member order).
+    {
+        const int wave = tid >> 6;
+#pragma unroll
+        for (int s = 0; s < kCentroids; ++s) {
+            const uint64_t m = __ballot(live && assign == s);
+            if ((tid & 63) == 0) slot_mask[wave][s] = m;
         }
     }
     __syncthreads();
-    if (live) {
-        int rank = 0;
-        for (int i = 0; i < tid; ++i) rank += assignment[i] == assign;
-        members[starts[assign] + rank] = tid;
-    }
-    __syncthreads();
-    if (tid < kCentroids) pops[row * kCentroids + tid] = static_cast<float>(counts[tid]);
+    if (tid < kCentroids)
+        pops[row * kCentroids + tid] =
+            static_cast<float>(__popcll(slot_mask[0][tid]) + __popcll(slot_mask[1][tid]));
 
     // Centroid = bf16(member sum / count), then the LSE pre-scale
     // bf16(centroid * 128^-0.5 * log2 e) (csrc/ibcs.cu:213-237, :293-295).
+    // Members are read 8 at a time; the sum adds them in query order (the
+    // unused tail of a group adds +0.0f, which leaves a sum that started at
+    // +0.0f unchanged).
     {
         uint16_t* dst = centroids + row * kCentroids * kHeadDim + tid;
         for (int s = 0; s < kCentroids; ++s) {
-            const int cnt = counts[s], first = starts[s];
             float sum = 0.0f;
-            for (int t = 0; t < cnt; ++t) sum += block_elem(block, members[first + t], tid);
+            int cnt = 0;
+#pragma unroll
+            for (int w = 0; w < kClusterThreads / 64; ++w) {
+                uint64_t m = slot_mask[w][s];
+                cnt += __popcll(m);
+                while (m != 0u) {
+                    int idx[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        idx[e] = m != 0u ? 64 * w + __builtin_ctzll(m) : -1;
+                        m &= m - 1u;
+                    }
+                    float v[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[e] = block_elem(block, max(idx[e], 0), tid);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) sum += idx[e] >= 0 ? v[e] : 0.0f;
+                }
+            }
             const uint32_t c = cnt > 0 ? f32_to_bf16(__fdiv_rn(sum, static_cast<float>(cnt))) : 0u;
             dst[s * kHeadDim] = static_cast<uint16_t>(f32_to_bf16(__uint_as_float(c << 16) * qk_scale_log2));
         }
@@ -248,9 +264,21 @@ __global__ __launch_bounds__(kMassThreads) void masses_kernel(
                                           fast_exp2(static_cast<float>(h[e]) - mx[s]) * inv_den[s],
                                           score[e]);
         }
+        // Two 16-byte stores (rows start at any multiple of 4 bytes, which
+        // global stores accept); the ragged end of the row element by element.
+        typedef float f32x4_u __attribute__((ext_vector_type(4), aligned(4)));
+        if (j0 + 8 <= fb) {
+            const f32x4_u lo = {score[0] * inv_total, score[1] * inv_total, score[2] * inv_total,
+                                score[3] * inv_total};
+            const f32x4_u hi = {score[4] * inv_total, score[5] * inv_total, score[6] * inv_total,
+                                score[7] * inv_total};
+            *reinterpret_cast<f32x4_u*>(dst + j0) = lo;
+            *reinterpret_cast<f32x4_u*>(dst + j0 + 4) = hi;
+        } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-            if (j0 + e < fb) dst[j0 + e] = score[e] * inv_total;
+            for (int e = 0; e < 8; ++e)
+                if (j0 + e < fb) dst[j0 + e] = score[e] * inv_total;
+        }
     }
 }
 

@@ -21,12 +21,12 @@
 // SIMD to hide LDS and fp64 latency.
 //
 // Two storage schemes, same bits:
-//   - sip_lds_kernel (rows whose clamped masses and fp64 prefixes fit in LDS):
+//   - sip_lds_kernel (rows whose masses and fp64 prefixes fit in LDS):
 //     persistent workgroups walk rows r, r + grid, ...; while a row is
-//     processed out of LDS, the next row's masses are already being loaded
-//     into registers in the thread-strided order of the first certainty
-//     pass, so that pass folds straight from registers. Certainty is marked
-//     by negating the LDS copy, as the reference does.
+//     processed out of LDS, the next row's masses are loaded into registers,
+//     and they are written to LDS as soon as the row's last draw has read it
+//     (before the row's results are stored). Certainty is marked by the sign
+//     bit of the LDS copy, as the reference negates its copy.
 //   - sip_global_kernel (larger rows): one row per workgroup, the row is
 //     re-read from L2 by each pass, LDS holds the prefixes and a certainty
 //     bitmask.
@@ -43,13 +43,38 @@ constexpr int kBucket = 4;
 constexpr int kUnroll = 8;
 constexpr int kDraws = 2;
 
-// Clamped masses held in LDS; the sign marks certainty.
+// Row accessors. raw(i) is the stored value of mass i, x_of() turns it into
+// the reference's clamped mass fmaxf(m, 1e-30f), certain_of() tells whether
+// the element is certain, weight_mass(i) is fmax((double)m, 1e-30) for the
+// log-weight. raw8(i0) fetches masses i0 .. i0+7 without bounds checks (the
+// storage is padded; callers discard indices >= population).
+
+// Masses held in LDS: negative and NaN masses are stored as +0 (the clamps
+// above map them to the same values), so the sign bit is free to mark
+// certainty, as the reference marks it by negating its copy.
 struct LdsRow {
-    const float* input;
-    float* values;
-    __device__ __forceinline__ float x(int i) const { return fabsf(values[i]); }
-    __device__ __forceinline__ bool certain(int i) const { return values[i] < 0.f; }
-    __device__ __forceinline__ void mark(int i) { values[i] = -values[i]; }
+    float* values;  // 16-byte aligned, population + 8 entries
+    __device__ __forceinline__ float raw(int i) const { return values[i]; }
+    __device__ __forceinline__ void raw8(int i0, float (&r)[8]) const {  // i0 % 4 == 0
+        const f32x4 a = *reinterpret_cast<const f32x4*>(values + i0);
+        const f32x4 b = *reinterpret_cast<const f32x4*>(values + i0 + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            r[e] = a[e];
+            r[e + 4] = b[e];
+        }
+    }
+    // fmaxf(|r|, 1e-30f) on the bit patterns: both are non-negative, non-NaN.
+    __device__ __forceinline__ static float x_of(float r) {
+        return __uint_as_float(max(__float_as_uint(r) & 0x7fffffffu, __float_as_uint(1e-30f)));
+    }
+    __device__ __forceinline__ bool certain_of(int, float r) const { return (__float_as_uint(r) >> 31) != 0u; }
+    __device__ __forceinline__ float x(int i) const { return x_of(values[i]); }
+    __device__ __forceinline__ bool certain(int i) const { return certain_of(i, values[i]); }
+    __device__ __forceinline__ void mark(int i) { values[i] = -fabsf(values[i]); }
+    __device__ __forceinline__ double weight_mass(int i) const {
+        return fmax(static_cast<double>(fabsf(values[i])), 1e-30);
+    }
     __device__ __forceinline__ void set_any_certain(bool) {}
 };
 
@@ -58,13 +83,28 @@ struct GlobalRow {
     const float* input;
     uint32_t* marks;
     bool any_certain;
-    __device__ __forceinline__ float x(int i) const { return fmaxf(input[i], 1e-30f); }
-    __device__ __forceinline__ bool certain(int i) const {
+    int last;  // population - 1
+    __device__ __forceinline__ float raw(int i) const { return input[i]; }
+    __device__ __forceinline__ void raw8(int i0, float (&r)[8]) const {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r[e] = input[min(i0 + e, last)];
+    }
+    __device__ __forceinline__ static float x_of(float r) { return fmaxf(r, 1e-30f); }
+    __device__ __forceinline__ bool certain_of(int i, float) const {
         return any_certain && ((marks[i >> 5] >> (i & 31)) & 1u);
     }
+    __device__ __forceinline__ float x(int i) const { return x_of(input[i]); }
+    __device__ __forceinline__ bool certain(int i) const { return certain_of(i, 0.f); }
     __device__ __forceinline__ void mark(int i) { atomicOr(&marks[i >> 5], 1u << (i & 31)); }
+    __device__ __forceinline__ double weight_mass(int i) const { return fmax(static_cast<double>(input[i]), 1e-30); }
     __device__ __forceinline__ void set_any_certain(bool v) { any_certain = v; }
 };
+
+// LDS layout of the row kernels: fp64 bucket prefixes [buckets + 1], then
+// (16-byte aligned) the masses or the certainty bitmask.
+__host__ __device__ constexpr size_t sip_values_offset(int64_t buckets) {
+    return (size_t(buckets + 1) * 8 + 15) / 16 * 16;
+}
 
 struct SipShared {
     double part[kSipThreads];
@@ -75,34 +115,39 @@ struct SipShared {
 };
 
 // Thread-strided partial (sum, max) over the non-certain masses: thread t
-// folds i = t, t+256, ... in order (sip.cu:63-71).
+// folds i = t, t+256, ... in order (sip.cu:63-71). The kUnroll loads of a
+// step are issued together (clamped indices), then folded.
 template <class R>
 __device__ __forceinline__ void strided_partials(const R& rv, int pop, double& sum, double& mx) {
     const int t = threadIdx.x;
     sum = 0.0;
-    mx = 0.0;
+    // The maximum is order free: kept as the bit pattern of the largest
+    // (positive) clamped mass, converted once at the end.
+    uint32_t top = 0u;
     for (int i0 = t; i0 < pop; i0 += kSipThreads * kUnroll) {
-        float v[kUnroll];
+        float r[kUnroll];
+#pragma unroll
+        for (int e = 0; e < kUnroll; ++e) r[e] = rv.raw(min(i0 + e * kSipThreads, pop - 1));
 #pragma unroll
         for (int e = 0; e < kUnroll; ++e) {
             const int i = i0 + e * kSipThreads;
-            v[e] = (i < pop && !rv.certain(i)) ? rv.x(i) : -1.0f;
+            const bool ok = i < pop && !rv.certain_of(i, r[e]);
+            const float x = R::x_of(r[e]);
+            sum = sum + (ok ? static_cast<double>(x) : 0.0);  // + 0.0 leaves a positive sum unchanged
+            top = max(top, ok ? __float_as_uint(x) : 0u);
         }
-#pragma unroll
-        for (int e = 0; e < kUnroll; ++e)
-            if (v[e] >= 0.0f) {
-                const double d = static_cast<double>(v[e]);
-                sum = sum + d;
-                mx = fmax(mx, d);
-            }
     }
+    mx = static_cast<double>(__uint_as_float(top));
 }
 
 // Everything after the first pass's thread partials are known: certainty
-// iteration, certain ids, chunk scan, bucket prefixes and the draws.
-template <class R>
-__device__ void sip_row(R& rv, double sum, double mx, double* prefix, SipShared& sh, float offset_u,
-                        int32_t* __restrict__ out_ids, float* __restrict__ out_w, int pop, int samples) {
+// iteration, certain ids, chunk scan, bucket prefixes and the draws. Inlined:
+// a called function starts by waiting for every outstanding memory access,
+// which would stall on the next row's prefetch.
+template <class R, class StageNext>
+__device__ __forceinline__ void sip_row(R& rv, double sum, double mx, double* prefix, SipShared& sh, float offset_u,
+                                        int32_t* __restrict__ out_ids, float* __restrict__ out_w, int pop,
+                                        int samples, StageNext stage_next) {
     const int t = threadIdx.x;
     const bool logical = t < kSipThreads;
     const int buckets = (pop + kBucket - 1) / kBucket;
@@ -202,19 +247,20 @@ __device__ void sip_row(R& rv, double sum, double mx, double* prefix, SipShared&
     }
 
     // Chunk masses and their CUB-ordered exclusive scan (sip.cu:126-130).
+    // A chunk starts at a multiple of 4; its masses are fetched 8 at a time.
+    // Positions past the chunk and certain blocks add 0.0, which leaves the
+    // (non-negative) running sum unchanged.
     if (logical) {
         double chunk_mass = 0.0;
-        for (int i0 = begin; i0 < end; i0 += kUnroll) {
-            float v[kUnroll];
+        for (int i0 = begin; i0 < end; i0 += 8) {
+            float r[8];
+            rv.raw8(i0, r);
 #pragma unroll
-            for (int e = 0; e < kUnroll; ++e) {
-                const int i = i0 + e;
-                v[e] = (i < end && !rv.certain(i)) ? rv.x(i) : -1.0f;
+            for (int e = 0; e < 8; ++e) {
+                const bool ok = i0 + e < end && !rv.certain_of(i0 + e, r[e]);
+                const double m = static_cast<double>(R::x_of(r[e])) * scale;
+                chunk_mass = chunk_mass + (ok ? m : 0.0);
             }
-#pragma unroll
-            for (int e = 0; e < kUnroll; ++e)
-                if (i0 + e < end)
-                    chunk_mass = chunk_mass + (v[e] < 0.0f ? 0.0 : static_cast<double>(v[e]) * scale);
         }
         sh.part[t] = chunk_mass;
     }
@@ -246,21 +292,17 @@ __device__ void sip_row(R& rv, double sum, double mx, double* prefix, SipShared&
     if (t == 0) prefix[buckets] = static_cast<double>(residuals);
     if (logical) {
         double cumulative = sh.part[t];
-        for (int i0 = begin; i0 < end; i0 += kUnroll) {
-            float v[kUnroll];
+        for (int i0 = begin; i0 < end; i0 += 8) {
+            float r[8];
+            rv.raw8(i0, r);
 #pragma unroll
-            for (int e = 0; e < kUnroll; ++e) {
+            for (int e = 0; e < 8; ++e) {
                 const int i = i0 + e;
-                v[e] = (i < end && !rv.certain(i)) ? rv.x(i) : -1.0f;
-            }
-#pragma unroll
-            for (int e = 0; e < kUnroll; ++e) {
-                const int i = i0 + e;
-                if (i < end) {
-                    if (i % kBucket == 0)
-                        prefix[i / kBucket] = i > last ? static_cast<double>(residuals) : cumulative;
-                    cumulative = cumulative + (v[e] < 0.0f ? 0.0 : static_cast<double>(v[e]) * scale);
-                }
+                if (e % kBucket == 0 && i < end)
+                    prefix[i / kBucket] = i > last ? static_cast<double>(residuals) : cumulative;
+                const bool ok = i < end && !rv.certain_of(i, r[e]);
+                const double m = static_cast<double>(R::x_of(r[e])) * scale;
+                cumulative = cumulative + (ok ? m : 0.0);
             }
         }
     }
@@ -268,9 +310,15 @@ __device__ void sip_row(R& rv, double sum, double mx, double* prefix, SipShared&
 
     // Systematic draws (sip.cu:144-166). Each thread runs up to kDraws
     // independent searches in lockstep (their LDS reads overlap); every search
-    // makes exactly the reference's probes.
+    // makes exactly the reference's probes. The results of the last round are
+    // stored only after stage_next() has refilled LDS with the next row (once
+    // every thread is done reading this one), so that the next row's prefetch
+    // never waits behind these stores.
     const double offset = static_cast<double>(offset_u);
-    for (int slot0 = t; slot0 < residuals; slot0 += kSipWorkers * kDraws) {
+    const int per_round = kSipWorkers * kDraws;
+    const int rounds = (residuals + per_round - 1) / per_round;
+    for (int round = 0; round < rounds; ++round) {
+        const int slot0 = t + round * per_round;
         int lower[kDraws], upper[kDraws];
         double threshold[kDraws];
 #pragma unroll
@@ -292,24 +340,42 @@ __device__ void sip_row(R& rv, double sum, double mx, double* prefix, SipShared&
                     busy = true;
                 }
         }
+        int selected[kDraws];
+        float weight[kDraws];
+#pragma unroll
+        for (int d = 0; d < kDraws; ++d) {
+            const int bucket = min(lower[d], buckets - 1);
+            double mass = prefix[bucket];
+            int sel = last;
+            float r[8];
+            rv.raw8(bucket * kBucket, r);
+#pragma unroll
+            for (int e = 0; e < kBucket; ++e) {
+                const int i = bucket * kBucket + e;
+                if (i >= pop || rv.certain_of(i, r[e])) continue;
+                sel = i;
+                mass = fma(static_cast<double>(R::x_of(r[e])), scale, mass);
+                if (mass > threshold[d]) break;
+            }
+            selected[d] = sel;
+            weight[d] = static_cast<float>(-log2(rv.weight_mass(sel) * scale));
+        }
+        if (round + 1 == rounds) {
+            __syncthreads();
+            stage_next();
+        }
 #pragma unroll
         for (int d = 0; d < kDraws; ++d) {
             const int slot = slot0 + d * kSipWorkers;
-            if (slot >= residuals) continue;
-            const int bucket = min(lower[d], buckets - 1);
-            double mass = prefix[bucket];
-            int selected = last;
-            const int stop = min((bucket + 1) * kBucket, pop);
-            for (int i = bucket * kBucket; i < stop; ++i) {
-                if (rv.certain(i)) continue;
-                selected = i;
-                mass = fma(static_cast<double>(rv.x(i)), scale, mass);
-                if (mass > threshold[d]) break;
+            if (slot < residuals) {
+                out_ids[certainty + slot] = selected[d];
+                out_w[certainty + slot] = weight[d];
             }
-            out_ids[certainty + slot] = selected;
-            out_w[certainty + slot] =
-                static_cast<float>(-log2(fmax(static_cast<double>(rv.input[selected]), 1e-30) * scale));
         }
+    }
+    if (rounds == 0) {
+        __syncthreads();
+        stage_next();
     }
 }
 
@@ -325,7 +391,7 @@ __global__ __launch_bounds__(kSipWorkers) void sip_lds_kernel(
     const int pop = population;
     const int buckets = (pop + kBucket - 1) / kBucket;
     double* prefix = reinterpret_cast<double*>(smem);
-    float* values = reinterpret_cast<float*>(prefix + buckets + 1);
+    float* values = reinterpret_cast<float*>(smem + sip_values_offset(buckets));
 
     float next[kPer];
     auto prefetch = [&](int64_t r) {
@@ -336,23 +402,29 @@ __global__ __launch_bounds__(kSipWorkers) void sip_lds_kernel(
             next[k] = i < pop ? in[i] : 0.0f;
         }
     };
-    int64_t row = blockIdx.x;
-    if (row < rows) prefetch(row);
-    for (; row < rows; row += gridDim.x) {
+    auto stage = [&] {
 #pragma unroll
         for (int k = 0; k < kPer; ++k) {
             const int i = t + k * kSipWorkers;
-            if (i < pop) values[i] = fmaxf(next[k], 1e-30f);
+            if (i < pop) values[i] = next[k] > 0.0f ? next[k] : 0.0f;  // NaN, negatives -> +0
         }
+    };
+    int64_t row = blockIdx.x;
+    if (row < rows) {
+        prefetch(row);
+        stage();
+    }
+    for (; row < rows; row += gridDim.x) {
         const int64_t following = row + gridDim.x;
         if (following < rows) prefetch(following);
-        __syncthreads();
-        LdsRow rv{masses + row * int64_t(pop), values};
+        __syncthreads();  // this row is staged
+        LdsRow rv{values};
         double sum = 0.0, mx = 0.0;
         if (t < kSipThreads) strided_partials(rv, pop, sum, mx);
         sip_row(rv, sum, mx, prefix, sh, offsets[row], ids + row * int64_t(samples),
-                logw + row * int64_t(samples), pop, samples);
-        __syncthreads();  // the next row overwrites values and prefixes
+                logw + row * int64_t(samples), pop, samples, [&] {
+                    if (following < rows) stage();
+                });
     }
 }
 
@@ -366,13 +438,13 @@ __global__ __launch_bounds__(kSipWorkers) void sip_global_kernel(
     const int pop = population;
     const int buckets = (pop + kBucket - 1) / kBucket;
     double* prefix = reinterpret_cast<double*>(smem);
-    GlobalRow rv{masses + row * int64_t(pop), reinterpret_cast<uint32_t*>(prefix + buckets + 1), false};
+    GlobalRow rv{masses + row * int64_t(pop), reinterpret_cast<uint32_t*>(prefix + buckets + 1), false, pop - 1};
     for (int w = t; w < (pop + 31) / 32; w += kSipWorkers) rv.marks[w] = 0u;
     __syncthreads();
     double sum = 0.0, mx = 0.0;
     if (t < kSipThreads) strided_partials(rv, pop, sum, mx);
     sip_row(rv, sum, mx, prefix, sh, offsets[row], ids + row * int64_t(samples), logw + row * int64_t(samples),
-            pop, samples);
+            pop, samples, [] {});
 }
 
 template <int kPer>
@@ -398,8 +470,8 @@ constexpr size_t kLdsLimit = 160 * 1024;
 
 size_t sip_lds_bytes(int64_t population, bool lds_values) {
     const int64_t buckets = (population + kBucket - 1) / kBucket;
-    const size_t base = size_t(buckets + 1) * 8;
-    return lds_values ? base + size_t(population) * 4 : base + size_t((population + 31) / 32) * 4;
+    const size_t base = sip_values_offset(buckets);
+    return lds_values ? base + size_t(population + 8) * 4 : base + size_t((population + 31) / 32) * 4;
 }
 
 bool sip_fits(int64_t population) { return sip_lds_bytes(population, false) + kSipStaticLds <= kLdsLimit; }
