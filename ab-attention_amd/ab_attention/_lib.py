@@ -32,6 +32,8 @@ SIGNATURES = {
     "ab_ibcs_masses": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _P, _P]),
     "ab_sip": (ctypes.c_int, [_P, _P, _I64, _I64, _I64, _P, _P, _P]),
     "ab_paged_prefill": (ctypes.c_int, [_P, _P, _P, _I64, _I64, _P, _P, _I64, _P, _P, _P]),
+    "ab_paged_prefill_kv": (ctypes.c_int, [_P, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _P, _P, _P]),
+    "ab_merge_states": (ctypes.c_int, [_P, _P, _P, _P, _I64, _P, _P, _P]),
 }
 
 ABI_VERSION = 1

@@ -73,3 +73,25 @@ def paged_attention(
     if not return_lse:
         return output
     return output, lse
+
+
+def _prefill_kv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
+                *, return_lse: bool = False):
+    """The weighted prefill with K/V of their own length (ab_paged_prefill_kv).
+
+    q bf16 [B,H,Nq,128], k/v bf16 [B,H,Nk,128] with Nk % 4 == 0, ids int32 /
+    weights f32 [B*H*ceil(Nq/128), S] with S % 8 == 0 (per-head KV4 ids; a -inf
+    weight removes its block). Shapes are checked by the callers.
+    """
+    batch, heads, tokens, _ = q.shape
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    ids = ids.to(torch.int32).contiguous()
+    weights = weights.to(torch.float32).contiguous()
+    output = torch.empty_like(q)
+    lse = torch.empty((batch, heads, tokens), dtype=torch.float32, device=q.device) if return_lse else None
+    lib = _lib.load()
+    with torch.cuda.device(q.device):
+        _lib.check(lib.ab_paged_prefill_kv(
+            _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), batch * heads, tokens, k.shape[2], _lib.ptr(ids),
+            _lib.ptr(weights), ids.shape[1], _lib.ptr(output), _lib.ptr(lse), _lib.stream(q.device)))
+    return (output, lse) if return_lse else output

@@ -1,4 +1,6 @@
-"""Video-layout helpers of the attention path.
+"""Video integration of the attention path: the cube token layout, exact
+(dense) attention, attention-state merging, the per-layer plan schedule and
+HunyuanVideo's text/video partition.
 
 ``cube_layout_order`` is the token permutation of the reference's
 ``use_cube_layout`` (ab_attention/video.py:90-126, order math :97-105): video
@@ -6,10 +8,28 @@ tokens grouped into 4x4x4 spatiotemporal cubes, cubes in (t, h, w) order,
 tokens inside a cube in (t, h, w) order, and boundary cubes holding only their
 valid tokens. The attention call itself sees ordinary [B, H, N, 128] tensors
 in cube order, so the kernels need nothing special for it.
+
+``exact_attention`` and ``merge_states`` stand for the reference's ``_exact``
+(FA3 dense prefill with base-2 LSE, video.py:13-28) and ``_merge``
+(FlashInfer merge_state, video.py:31-40); both run on this library's kernels.
+``VideoAttention`` is the reference's denoising schedule (video.py:53-87) with
+the plans kept on the GPU. ``hunyuan_attention`` is ``_hunyuan_attention``
+(video.py:129-151): by default the video queries attend to their sampled pages
+and to every text block (weight 0) in one prefill, which equals the
+reference's sampled state merged with the exact text state.
 """
 from __future__ import annotations
 
+import math
+
 import torch
+
+from . import _lib
+from .attention import SamplePlan, apply_plan, build_plan
+from .paged import _prefill_kv
+
+_QUERY_BLOCK = 128
+_PAGE = 4
 
 
 def cube_layout_order(num_frames: int, height: int, width: int):
@@ -36,3 +56,143 @@ def cube_order(grid):
     inner = ((tt % 4) * 4 + hh % 4) * 4 + ww % 4
     order = torch.argsort((cube * 64 + inner).reshape(-1))
     return order, torch.argsort(order)
+
+
+def _check_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
+    if q.ndim != 4 or k.ndim != 4 or k.shape != v.shape or q.shape[:2] != k.shape[:2]:
+        raise ValueError("Q [B,H,Nq,128] and K/V [B,H,Nk,128] must share batch and heads")
+    if q.shape[-1] != 128 or k.shape[-1] != 128:
+        raise ValueError("attention requires head_dim=128")
+    if q.device.type != "cuda" or k.device != q.device or v.device != q.device:
+        raise ValueError("Q/K/V must be on the same CUDA device")
+    if q.dtype != torch.bfloat16 or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("attention requires BF16 Q/K/V")
+    if k.shape[2] % _PAGE:
+        raise ValueError("the key/value length must be divisible by 4")
+
+
+def _dense_pages(rows: int, blocks: int, device, offset: int = 0):
+    """ids/weights listing KV4 blocks offset .. offset+blocks-1 at weight 0 for
+    every row, padded to a multiple of 8 with -inf-weight repeats of the first."""
+    samples = -(-blocks // 8) * 8
+    ids = torch.full((samples,), offset, dtype=torch.int32, device=device)
+    ids[:blocks] = torch.arange(offset, offset + blocks, dtype=torch.int32, device=device)
+    weights = torch.full((samples,), float("-inf"), dtype=torch.float32, device=device)
+    weights[:blocks] = 0.0
+    return ids.expand(rows, samples).contiguous(), weights.expand(rows, samples).contiguous()
+
+
+@torch.no_grad()
+def exact_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, return_lse: bool = False):
+    """Dense non-causal attention of q [B,H,Nq,128] over k/v [B,H,Nk,128]
+    (bf16, Nk divisible by 4); returns o bf16 [B,H,Nq,128] (and the base-2
+    lse f32 [B,H,Nq]). The reference's _exact (video.py:13-28) on this
+    library's prefill: every KV4 block of K/V listed at weight 0."""
+    _check_qkv(q, k, v)
+    batch, heads, tokens, _ = q.shape
+    rows = batch * heads * math.ceil(tokens / _QUERY_BLOCK)
+    ids, weights = _dense_pages(rows, k.shape[2] // _PAGE, q.device)
+    return _prefill_kv(q, k, v, ids, weights, return_lse=return_lse)
+
+
+@torch.no_grad()
+def merge_states(state_a, state_b, *, return_lse: bool = False):
+    """Merge two attention states over disjoint key sets: (o bf16 [B,H,N,128],
+    lse f32 [B,H,N] base 2) each. Returns the merged o (and lse). The
+    reference's _merge (video.py:31-40, FlashInfer merge_state)."""
+    (o_a, s_a), (o_b, s_b) = state_a, state_b
+    if o_a.shape != o_b.shape or o_a.shape[-1] != 128 or s_a.shape != o_a.shape[:-1] or s_b.shape != s_a.shape:
+        raise ValueError("states must be o [..., 128] with lse [...] of matching shapes")
+    if o_a.dtype != torch.bfloat16 or o_b.dtype != o_a.dtype:
+        raise ValueError("merge_states requires BF16 outputs")
+    if o_a.device.type != "cuda" or o_b.device != o_a.device or s_a.device != o_a.device or s_b.device != o_a.device:
+        raise ValueError("states must be on the same CUDA device")
+    o_a, o_b = o_a.contiguous(), o_b.contiguous()
+    s_a, s_b = s_a.to(torch.float32).contiguous(), s_b.to(torch.float32).contiguous()
+    out = torch.empty_like(o_a)
+    lse = torch.empty_like(s_a) if return_lse else None
+    lib = _lib.load()
+    with torch.cuda.device(o_a.device):
+        _lib.check(lib.ab_merge_states(_lib.ptr(o_a), _lib.ptr(s_a), _lib.ptr(o_b), _lib.ptr(s_b), s_a.numel(),
+                                       _lib.ptr(out), _lib.ptr(lse), _lib.stream(o_a.device)))
+    return (out, lse) if return_lse else out
+
+
+class VideoAttention:
+    """One pipeline's denoising schedule and per-layer sample plans
+    (reference: video.py:53-87). Steps 1-10 and layer 0 stay dense; other
+    layers build a plan on steps 11, 15, ..., and reuse it in between. The
+    plans stay on the GPU (the reference parks them in pinned host memory).
+    """
+
+    def __init__(self, sample_pages: int, *, dense: bool = False):
+        self.sample_pages = sample_pages
+        self.dense = dense
+        self.reset()
+
+    def reset(self):
+        self.step = 1
+        self.plans = {}
+
+    def step_end(self, pipe, index, timestep, callback_kwargs):
+        self.step = index + 2  # Diffusers indices are zero-based.
+        return callback_kwargs
+
+    def is_sparse(self, layer: int) -> bool:
+        return not self.dense and self.step > 10 and layer > 0
+
+    def plan(self, layer: int, q: torch.Tensor, k: torch.Tensor) -> SamplePlan:
+        """The layer's plan for the current step: built at each anchor step
+        (seed 42 + layer*1000003 + anchor*97, as the reference), else reused."""
+        anchor = 11 + (self.step - 11) // 4 * 4
+        stored_anchor, stored = self.plans.get(layer, (None, None))
+        if stored_anchor != anchor or stored.descriptor.device != q.device:
+            seed = 42 + layer * 1_000_003 + anchor * 97
+            stored = build_plan(q, k, sample_pages=self.sample_pages, seed=seed)
+            self.plans[layer] = (anchor, stored)
+        return stored
+
+    def attend(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, return_lse: bool = False):
+        return apply_plan(q, k, v, self.plan(layer, q, k), return_lse=return_lse)
+
+
+@torch.no_grad()
+def hunyuan_attention(schedule: VideoAttention, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                      video_tokens: int, prompt_tokens: int, *, fused: bool = True) -> torch.Tensor:
+    """HunyuanVideo attention over [video | prompt | padding] tokens
+    (reference: _hunyuan_attention, video.py:129-151). On sparse steps video
+    queries use the sampled plan over video keys plus every prompt key; prompt
+    queries attend densely to video and prompt keys; padding tokens attend
+    among themselves. With ``fused`` (default) the video queries' sampled and
+    prompt parts run as one prefill (the prompt blocks listed at weight 0);
+    otherwise as the reference: sampled state, exact prompt state, merge."""
+    _check_qkv(q, k, v)
+    if q.shape != k.shape:
+        raise ValueError("Q/K/V must have the same [B,H,N,D] shape")
+    tokens = q.shape[2]
+    prompt_end = video_tokens + prompt_tokens
+    if video_tokens % _PAGE or prompt_tokens % _PAGE or (tokens - prompt_end) % _PAGE or prompt_end > tokens:
+        raise ValueError("video, prompt and padding lengths must be divisible by 4 and fit in N")
+    if not schedule.is_sparse(layer):
+        outputs = [exact_attention(q[:, :, :prompt_end], k[:, :, :prompt_end], v[:, :, :prompt_end])]
+    else:
+        q_video = q[:, :, :video_tokens].contiguous()
+        k_video = k[:, :, :video_tokens].contiguous()
+        k_prompt, v_prompt = k[:, :, :prompt_end].contiguous(), v[:, :, :prompt_end].contiguous()
+        if fused:
+            plan = schedule.plan(layer, q_video, k_video)
+            rows = plan.descriptor.shape[0]
+            text_ids, text_w = _dense_pages(rows, prompt_tokens // _PAGE, q.device, offset=video_tokens // _PAGE)
+            ids = torch.cat([plan.descriptor.reshape(rows, -1), text_ids], dim=1)
+            weights = torch.cat([plan.log_weights.reshape(rows, -1), text_w], dim=1)
+            video_out = _prefill_kv(q_video, k_prompt, v_prompt, ids, weights)
+        else:
+            video_state = schedule.attend(layer, q_video, k_video, v[:, :, :video_tokens].contiguous(),
+                                          return_lse=True)
+            text_state = exact_attention(q_video, k[:, :, video_tokens:prompt_end], v[:, :, video_tokens:prompt_end],
+                                         return_lse=True)
+            video_out = merge_states(video_state, text_state)
+        outputs = [video_out, exact_attention(q[:, :, video_tokens:prompt_end], k_prompt, v_prompt)]
+    if prompt_end < tokens:
+        outputs.append(exact_attention(q[:, :, prompt_end:], k[:, :, prompt_end:], v[:, :, prompt_end:]))
+    return torch.cat(outputs, dim=2)

@@ -23,8 +23,11 @@ int launch_masses(const void* lse, const float* pops, const float* lse_max, cons
 int launch_sip(const float* scores, const float* offsets, int64_t rows, int64_t population, int64_t samples,
                int32_t* ids, float* logw, hipStream_t stream);
 bool sip_fits(int64_t population);
-int launch_prefill(const void* q, const void* k, const void* v, int64_t bh, int64_t n, const int32_t* ids,
-                   const float* logw, int64_t samples, void* out, float* lse, hipStream_t stream);
+int launch_prefill(const void* q, const void* k, const void* v, int64_t bh, int64_t n, int64_t n_kv,
+                   const int32_t* ids, const float* logw, int64_t samples, void* out, float* lse,
+                   hipStream_t stream);
+int launch_merge(const void* oa, const float* sa, const void* ob, const float* sb, int64_t count, void* out,
+                 float* s_out, hipStream_t stream);
 
 namespace {
 thread_local char g_error[512] = "";
@@ -185,14 +188,43 @@ int ab_paged_prefill(const void* q, const void* k, const void* v, int64_t batch_
     if (int rc = check_qk_shape("paged_prefill", batch_heads, tokens)) return rc;
     if (samples <= 0 || samples % kBlocksPerPage)
         return set_error(AB_ERR_INVALID, "paged_prefill: samples must be a positive multiple of 32");
+    return ab_paged_prefill_kv(q, k, v, batch_heads, tokens, tokens, ids, log_weights, samples, out, lse, stream);
+}
+
+int ab_paged_prefill_kv(const void* q, const void* k, const void* v, int64_t batch_heads, int64_t q_tokens,
+                        int64_t kv_tokens, const int32_t* ids, const float* log_weights, int64_t samples,
+                        void* out, float* lse, void* stream) {
+    if (batch_heads <= 0 || q_tokens <= 0 || kv_tokens <= 0)
+        return set_error(AB_ERR_INVALID, "paged_prefill: batch_heads and token counts must be positive");
+    if (kv_tokens % kKvBlock)
+        return set_error(AB_ERR_INVALID, "paged_prefill: key/value length must be divisible by 4");
+    if (kv_tokens * kHeadDim * 2 > int64_t(0xffffffff))
+        return set_error(AB_ERR_INVALID, "paged_prefill: one head of K/V must be under 4 GiB");
+    const int64_t qb = (q_tokens + kQueryBlock - 1) / kQueryBlock;
+    if (batch_heads > 65535 || qb > 65535) return set_error(AB_ERR_INVALID, "paged_prefill: grid too large");
+    if (samples <= 0 || samples % 8)
+        return set_error(AB_ERR_INVALID, "paged_prefill: samples must be a positive multiple of 8");
     if (!q || !k || !v || !ids || !log_weights || !out)
         return set_error(AB_ERR_INVALID, "paged_prefill: null pointer");
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || (reinterpret_cast<uintptr_t>(out) & 7u))
         return set_error(AB_ERR_INVALID, "paged_prefill: q/k/v must be 16-byte and out 8-byte aligned");
-    const int64_t rows = batch_heads * ((tokens + kQueryBlock - 1) / kQueryBlock);
-    if (rows * 8 > 0xffffffffll) return set_error(AB_ERR_INVALID, "paged_prefill: too many rows");
-    return launch_prefill(q, k, v, batch_heads, tokens, ids, log_weights, samples, out, lse,
+    if (!aligned16(ids) || !aligned16(log_weights))
+        return set_error(AB_ERR_INVALID, "paged_prefill: ids and log_weights must be 16-byte aligned");
+    const int64_t rows = batch_heads * qb;
+    if (rows * samples > (int64_t(1) << 40)) return set_error(AB_ERR_INVALID, "paged_prefill: plan too large");
+    return launch_prefill(q, k, v, batch_heads, q_tokens, kv_tokens, ids, log_weights, samples, out, lse,
                           static_cast<hipStream_t>(stream));
+}
+
+int ab_merge_states(const void* o_a, const float* lse_a, const void* o_b, const float* lse_b, int64_t count,
+                    void* out, float* lse_out, void* stream) {
+    if (count < 0) return set_error(AB_ERR_INVALID, "merge_states: negative count");
+    if (count > 0 && (!o_a || !lse_a || !o_b || !lse_b || !out))
+        return set_error(AB_ERR_INVALID, "merge_states: null pointer");
+    if (!aligned16(o_a) || !aligned16(o_b) || !aligned16(out))
+        return set_error(AB_ERR_INVALID, "merge_states: states must be 16-byte aligned");
+    if (count > (int64_t(1) << 35)) return set_error(AB_ERR_INVALID, "merge_states: too many rows");
+    return launch_merge(o_a, lse_a, o_b, lse_b, count, out, lse_out, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -3,7 +3,8 @@
 // Computes, for every 128-query row of the plan and every valid query i,
 //   z_t = q_i . k_t * log2(e)/sqrt(128) + w_j      (key t in KV4 block j)
 //   o_i = sum_t 2^(z_t - m) v_t / sum_t 2^(z_t - m),  lse_i = m + log2(sum_t 2^(z_t - m))
-// over exactly the row's S sampled KV4 blocks (4S keys). This is the
+// over exactly the row's S listed KV4 blocks (4S keys) of the head's K/V,
+// which may be longer or shorter than Q (n_kv tokens). This is the
 // ABSipAttention variant of the reference's FlashInfer prefill
 // (ab_attention/flashinfer_backend.py:30-59): logits + w / (sm_scale*log2 e),
 // then an online softmax in base 2 with scale sm_scale*log2 e.
@@ -89,7 +90,8 @@ __device__ __forceinline__ void wait_and_barrier() {
 __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const int32_t* __restrict__ ids, const float* __restrict__ logw, uint16_t* __restrict__ out,
-    float* __restrict__ lse, int64_t n, int64_t qb, int64_t rows, int fb, int samples, float scale_log2) {
+    float* __restrict__ lse, int64_t n, int64_t n_kv, int64_t qb, int64_t rows, int fb, int samples,
+    float scale_log2) {
     extern __shared__ __align__(16) unsigned char smem[];
 
     // XCD-aware row order. The hardware deals workgroups round-robin over the
@@ -127,8 +129,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
     const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)smem));
     const int32_t* row_ids = ids + row * int64_t(samples);
     const float* row_w = logw + row * int64_t(samples);
-    const uint16_t* kbase = k + bh * n * kHeadDim;
-    const uint16_t* vbase = v + bh * n * kHeadDim;
+    const uint16_t* kbase = k + bh * n_kv * kHeadDim;
+    const uint16_t* vbase = v + bh * n_kv * kHeadDim;
 
     // Batch b of ids and weights (tiles 64b .. 64b+63) into buffer b & 1, by
     // wave 0: two 1 KiB transfers each. Lanes past the row's end re-read its
@@ -308,17 +310,56 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
     }
 }
 
+// Merge of two attention states over disjoint key sets (base-2 LSEs), as
+// FlashInfer's merge_state: m = max(s_a, s_b), w = 2^(s - m),
+// o = (o_a w_a + o_b w_b) / (w_a + w_b), s = m + log2(w_a + w_b), in fp32.
+// One thread per 8 dims (16 bytes) of one query's 128-dim row.
+__global__ __launch_bounds__(256) void merge_kernel(const uint16_t* __restrict__ oa, const float* __restrict__ sa,
+                                                   const uint16_t* __restrict__ ob, const float* __restrict__ sb,
+                                                   int64_t count, uint16_t* __restrict__ out,
+                                                   float* __restrict__ s_out) {
+    const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t row = idx >> 4, part = idx & 15;
+    if (row >= count) return;
+    const float a = sa[row], b = sb[row];
+    const float m = fmaxf(a, b);
+    const float wa = fast_exp2(a - m), wb = fast_exp2(b - m);
+    const float d = wa + wb, inv = 1.0f / d;
+    const u32x4 va = reinterpret_cast<const u32x4*>(oa + row * kHeadDim)[part];
+    const u32x4 vb = reinterpret_cast<const u32x4*>(ob + row * kHeadDim)[part];
+    u32x4 r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float lo = (bf16_lo(va[e]) * wa + bf16_lo(vb[e]) * wb) * inv;
+        const float hi = (bf16_hi(va[e]) * wa + bf16_hi(vb[e]) * wb) * inv;
+        r[e] = pack_bf16(lo, hi);
+    }
+    reinterpret_cast<u32x4*>(out + row * kHeadDim)[part] = r;
+    if (s_out != nullptr && part == 0) s_out[row] = m + log2f(d);
+}
+
 }  // namespace
 
-int launch_prefill(const void* q, const void* k, const void* v, int64_t bh, int64_t n, const int32_t* ids,
-                   const float* logw, int64_t samples, void* out, float* lse, hipStream_t stream) {
+int launch_merge(const void* oa, const float* sa, const void* ob, const float* sb, int64_t count, void* out,
+                 float* s_out, hipStream_t stream) {
+    if (count == 0) return 0;
+    const int64_t threads = count * 16;
+    hipLaunchKernelGGL(merge_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, stream,
+                       static_cast<const uint16_t*>(oa), sa, static_cast<const uint16_t*>(ob), sb, count,
+                       static_cast<uint16_t*>(out), s_out);
+    return check_launch("merge_kernel");
+}
+
+int launch_prefill(const void* q, const void* k, const void* v, int64_t bh, int64_t n, int64_t n_kv,
+                   const int32_t* ids, const float* logw, int64_t samples, void* out, float* lse,
+                   hipStream_t stream) {
     const int64_t qb = (n + kQueryBlock - 1) / kQueryBlock;
     const int64_t rows = bh * qb;
     if (samples % kTilePages != 0)
         return set_error(1, "prefill: samples (%lld) must be a multiple of %d", (long long)samples, kTilePages);
     if ((reinterpret_cast<uintptr_t>(ids) & 15u) || (reinterpret_cast<uintptr_t>(logw) & 15u))
         return set_error(1, "prefill: ids and log_weights must be 16-byte aligned");
-    if (n * kHeadDim * 2 > int64_t(0xffffffff))
+    if (n_kv * kHeadDim * 2 > int64_t(0xffffffff))
         return set_error(1, "prefill: one head of K/V must be under 4 GiB");
     const float scale_log2 = static_cast<float>(1.4426950408889634 / 11.313708498984761);  // log2(e)/sqrt(128)
     const int64_t per_xcd = (qb + 7) / 8;
@@ -331,8 +372,8 @@ int launch_prefill(const void* q, const void* k, const void* v, int64_t bh, int6
     if (rows == 0) return 0;
     hipLaunchKernelGGL(prefill_kernel, dim3(static_cast<unsigned>(per_xcd * 8 * bh)), dim3(kPfThreads), kLdsBytes,
                        stream, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
-                       static_cast<const uint16_t*>(v), ids, logw, static_cast<uint16_t*>(out), lse, n, qb, rows,
-                       static_cast<int>(n / kKvBlock), static_cast<int>(samples), scale_log2);
+                       static_cast<const uint16_t*>(v), ids, logw, static_cast<uint16_t*>(out), lse, n, n_kv, qb, rows,
+                       static_cast<int>(n_kv / kKvBlock), static_cast<int>(samples), scale_log2);
     return check_launch("prefill_kernel");
 }
 

@@ -86,6 +86,25 @@ int ab_paged_prefill(const void *q, const void *k, const void *v, int64_t batch_
                      const int32_t *ids, const float *log_weights, int64_t samples, void *out, float *lse,
                      void *stream);
 
+/* The same prefill with a K/V length of its own (kv_tokens, divisible by 4)
+ * and any positive multiple of 8 for samples (a listed block may carry a
+ * -inf weight, which removes it). With every block of K/V listed at weight 0
+ * this is dense attention: it replaces the FA3 single prefill of _exact
+ * (ab_attention/video.py:13-28); with a plan's ids plus the text blocks at
+ * weight 0 it computes _hunyuan_attention's video state and its merge with
+ * the exact text state in one pass (video.py:129-142). */
+int ab_paged_prefill_kv(const void *q, const void *k, const void *v, int64_t batch_heads, int64_t q_tokens,
+                        int64_t kv_tokens, const int32_t *ids, const float *log_weights, int64_t samples,
+                        void *out, float *lse, void *stream);
+
+/* ---- Attention-state merge -------------------------------------------------
+ * Replaces FlashInfer's merge_state as used by _merge
+ * (ab_attention/video.py:31-40): two states over disjoint key sets, o bf16
+ * [count, 128] with base-2 lse f32 [count] -> merged o bf16 [count, 128] and,
+ * if lse_out != NULL, the merged lse. */
+int ab_merge_states(const void *o_a, const float *lse_a, const void *o_b, const float *lse_b, int64_t count,
+                    void *out, float *lse_out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

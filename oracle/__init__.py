@@ -59,6 +59,8 @@ def lib():
         _lib.orc_sip.restype = ctypes.c_int
         _lib.orc_prefill.argtypes = [_P, _P, _P, _I64, _I64, _P, _P, _I64, _P, _I64, _P, _P]
         _lib.orc_prefill.restype = ctypes.c_int
+        _lib.orc_prefill_kv.argtypes = [_P, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _P, _P]
+        _lib.orc_prefill_kv.restype = ctypes.c_int
         _lib.orc_f32_to_f16.argtypes = [ctypes.c_float]
         _lib.orc_f32_to_f16.restype = ctypes.c_uint16
         _lib.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
@@ -165,12 +167,14 @@ def sip(scores: np.ndarray, offsets: np.ndarray, samples: int):
 
 
 def prefill(q: np.ndarray, k: np.ndarray, v: np.ndarray, ids: np.ndarray, logw: np.ndarray, rows=None):
-    """Exact weighted sparse attention. q/k/v float32 [bh, n, 128]; ids/logw [rows, S].
+    """Exact weighted sparse attention. q float32 [bh, n, 128]; k/v float32
+    [bh, n_kv, 128] (n_kv may differ from n); ids/logw [rows, S], rows = bh*ceil(n/128).
 
     Returns (out float32 [bh, n, 128], lse float32 [bh, n], base 2). With
     ``rows`` (row indices) only those rows' queries are computed; the other
-    outputs are NaN."""
+    outputs are NaN. A -inf weight removes its block."""
     bh, n, _ = q.shape
+    n_kv = k.shape[1]
     q, k, v = (np.ascontiguousarray(t, np.float32) for t in (q, k, v))
     nrows = ids.shape[0]
     ids = np.ascontiguousarray(ids.reshape(nrows, -1), np.int32)
@@ -178,12 +182,28 @@ def prefill(q: np.ndarray, k: np.ndarray, v: np.ndarray, ids: np.ndarray, logw: 
     out = np.full_like(q, np.nan)
     lse_out = np.full((bh, n), np.nan, np.float32)
     row_arr = None if rows is None else np.ascontiguousarray(rows, np.int64)
-    rc = lib().orc_prefill(_ptr(q), _ptr(k), _ptr(v), bh, n, _ptr(ids), _ptr(logw), ids.shape[1],
-                           None if row_arr is None else _ptr(row_arr),
-                           0 if row_arr is None else len(row_arr), _ptr(out), _ptr(lse_out))
+    rc = lib().orc_prefill_kv(_ptr(q), _ptr(k), _ptr(v), bh, n, n_kv, _ptr(ids), _ptr(logw), ids.shape[1],
+                              None if row_arr is None else _ptr(row_arr),
+                              0 if row_arr is None else len(row_arr), _ptr(out), _ptr(lse_out))
     if rc:
         raise ValueError("plan id or row outside range")
     return out, lse_out
+
+
+def merge_states(o_a: np.ndarray, s_a: np.ndarray, o_b: np.ndarray, s_b: np.ndarray):
+    """Merge of two attention states over disjoint key sets, base-2 LSEs, in
+    float64: FlashInfer's merge_state (flashinfer-python 0.6.12, used by
+    ab_attention/video.py:31-40; not vendored under the reference):
+        m = max(s_a, s_b), w = 2^(s - m), o = (o_a w_a + o_b w_b) / (w_a + w_b),
+        s = m + log2(w_a + w_b).
+    o_*: [..., 128], s_*: [...]. Returns (o float64, s float64)."""
+    s_a = np.asarray(s_a, np.float64)
+    s_b = np.asarray(s_b, np.float64)
+    m = np.maximum(s_a, s_b)
+    w_a, w_b = np.exp2(s_a - m), np.exp2(s_b - m)
+    d = w_a + w_b
+    o = (np.asarray(o_a, np.float64) * w_a[..., None] + np.asarray(o_b, np.float64) * w_b[..., None]) / d[..., None]
+    return o, m + np.log2(d)
 
 
 def f32_to_f16_bits(x: float) -> int:

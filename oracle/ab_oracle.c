@@ -511,17 +511,18 @@ int orc_sip(const float *scores, const float *offsets, int64_t rows, int64_t pop
  * Exact (double) evaluation of the ABSipAttention variant:
  *   o_i = sum_j 2^{w_j} sum_{t in block j} e^{q_i.k_t/sqrt(128)} v_t / (same without v_t)
  *   lse_i = log2(sum_j 2^{w_j} sum_t e^{q_i.k_t/sqrt(128)})           (base 2)
- * q, k, v: float [bh, n, 128] (bf16 inputs widened by the caller);
+ * q: float [bh, n, 128], k, v: float [bh, n_kv, 128] (bf16 inputs widened by
+ * the caller); a -inf weight removes its block;
  * ids, logw: [rows, samples] per-head KV4 ids and log2 weights, rows = bh*qb.
  * out: float [bh, n, 128]; lse: float [bh, n] or NULL. Padded queries of the
  * last block are not produced (the reference computes and drops them).
  * row_list (optional, row_count entries) restricts the work to those rows;
  * outputs of other rows are left untouched.
  */
-int orc_prefill(const float *q, const float *k, const float *v, int64_t bh_count, int64_t n,
-                const int32_t *ids, const float *logw, int64_t samples, const int64_t *row_list,
-                int64_t row_count, float *out, float *lse) {
-    const int64_t qb = (n + QUERY_BLOCK - 1) / QUERY_BLOCK, fb = n / KV_BLOCK;
+int orc_prefill_kv(const float *q, const float *k, const float *v, int64_t bh_count, int64_t n,
+                   int64_t n_kv, const int32_t *ids, const float *logw, int64_t samples,
+                   const int64_t *row_list, int64_t row_count, float *out, float *lse) {
+    const int64_t qb = (n + QUERY_BLOCK - 1) / QUERY_BLOCK, fb = n_kv / KV_BLOCK;
     const int64_t keys = samples * KV_BLOCK;
     double *logit = malloc(sizeof(double) * (size_t)keys);
     if (!logit) return 1;
@@ -549,7 +550,7 @@ int orc_prefill(const float *q, const float *k, const float *v, int64_t bh_count
                         return 2;
                     }
                     for (int t = 0; t < KV_BLOCK; ++t) {
-                        const float *kt = k + (bh * n + KV_BLOCK * j + t) * HEAD_DIM;
+                        const float *kt = k + (bh * n_kv + KV_BLOCK * j + t) * HEAD_DIM;
                         double dot = 0.0;
                         for (int d = 0; d < HEAD_DIM; ++d) dot += (double)qi[d] * (double)kt[d];
                         const double z = dot * scale + (double)rw[s] * ln2;
@@ -562,7 +563,7 @@ int orc_prefill(const float *q, const float *k, const float *v, int64_t bh_count
                     const int64_t j = rid[s];
                     for (int t = 0; t < KV_BLOCK; ++t) {
                         const double p = exp(logit[s * KV_BLOCK + t] - mx);
-                        const float *vt = v + (bh * n + KV_BLOCK * j + t) * HEAD_DIM;
+                        const float *vt = v + (bh * n_kv + KV_BLOCK * j + t) * HEAD_DIM;
                         den += p;
                         for (int d = 0; d < HEAD_DIM; ++d) acc[d] += p * (double)vt[d];
                     }
@@ -575,4 +576,11 @@ int orc_prefill(const float *q, const float *k, const float *v, int64_t bh_count
     }
     free(logit);
     return 0;
+}
+
+/* Q and K/V of the same length (the plan's case). */
+int orc_prefill(const float *q, const float *k, const float *v, int64_t bh_count, int64_t n,
+                const int32_t *ids, const float *logw, int64_t samples, const int64_t *row_list,
+                int64_t row_count, float *out, float *lse) {
+    return orc_prefill_kv(q, k, v, bh_count, n, n, ids, logw, samples, row_list, row_count, out, lse);
 }

@@ -79,3 +79,39 @@ def test_heads_per_chunk_budget():
     # Wan2.1-14B 720p runs as one chunk within the 16 GiB budget
     assert _heads_per_chunk(80, 591, 75600) == 80
     assert _heads_per_chunk(4, 10, 1280) == 4
+
+
+def test_dense_page_list_padding():
+    """Dense page lists (exact attention, Hunyuan prompt blocks): every block
+    once at weight 0, padded to a multiple of 8 with removed (-inf) repeats."""
+    import torch
+    from ab_attention.video import _dense_pages
+
+    ids, w = _dense_pages(3, 10, "cpu", offset=5)
+    assert ids.shape == (3, 16) and w.shape == (3, 16)
+    assert ids[0, :10].tolist() == list(range(5, 15)) and ids[0, 10:].tolist() == [5] * 6
+    assert torch.all(w[:, :10] == 0) and torch.all(torch.isinf(w[:, 10:])) and torch.all(w[:, 10:] < 0)
+    assert torch.equal(ids[2], ids[0])
+    ids, w = _dense_pages(1, 64, "cpu")
+    assert ids.shape == (1, 64) and torch.all(w == 0)
+
+
+def test_video_validation_errors():
+    import pytest
+    import torch
+    from ab_attention.video import VideoAttention, exact_attention, hunyuan_attention, merge_states
+
+    q = torch.zeros(1, 2, 64, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        exact_attention(q, q[:, :, :62], q[:, :, :62])  # K/V length not divisible by 4
+    with pytest.raises(ValueError):
+        exact_attention(q, q, q)  # CPU tensors
+    with pytest.raises(ValueError):
+        hunyuan_attention(VideoAttention(1), 1, q, q, q, 30, 32)  # video length not divisible by 4
+    with pytest.raises(ValueError):
+        merge_states((q, torch.zeros(1, 2, 64)), (q, torch.zeros(1, 2, 63)))
+    sched = VideoAttention(4)
+    assert not sched.is_sparse(1)
+    sched.step = 11
+    assert sched.is_sparse(1) and not sched.is_sparse(0)
+    assert not VideoAttention(4, dense=True).is_sparse(3)

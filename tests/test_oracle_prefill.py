@@ -97,3 +97,46 @@ def test_row_subset(oracle_mod):
     sub, ls = oracle_mod.prefill(q, k, v, ids, w, rows=[2])
     np.testing.assert_array_equal(sub[0, 256:384], full[0, 256:384])
     assert np.isnan(sub[0, :256]).all()
+
+
+def test_separate_kv_length_matches_dense_softmax(oracle_mod):
+    """K/V of their own length (the text partition of video.py:129-151): all
+    blocks at weight 0 is dense softmax attention of Nq queries over Nk keys;
+    a -inf weight removes its block."""
+    rng = np.random.default_rng(4)
+    nq, nk = 200, 96
+    q = rng.normal(0, 1, (1, nq, 128)).astype(np.float32)
+    k = rng.normal(0, 1, (1, nk, 128)).astype(np.float32)
+    v = rng.normal(0, 1, (1, nk, 128)).astype(np.float32)
+    rows, fb = -(-nq // 128), nk // 4
+    ids = np.tile(np.r_[np.arange(fb), [0, 0]].astype(np.int32), (rows, 1))  # two removed repeats
+    logw = np.tile(np.r_[np.zeros(fb), [-np.inf, -np.inf]].astype(np.float32), (rows, 1))
+    o, l = oracle_mod.prefill(q, k, v, ids, logw)
+    z = q[0].astype(np.float64) @ k[0].astype(np.float64).T / np.sqrt(128)
+    p = np.exp(z - z.max(1, keepdims=True))
+    np.testing.assert_allclose(o[0], p @ v[0] / p.sum(1, keepdims=True), rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(l[0], (z.max(1) + np.log(p.sum(1))) / np.log(2), rtol=1e-6, atol=1e-5)
+
+
+def test_merge_of_disjoint_partitions_is_attention_over_union(oracle_mod):
+    """FlashInfer merge_state restated: merging the states of two disjoint
+    key sets equals attention over their union (the identity that lets the
+    Hunyuan text keys ride in the video prefill at weight 0)."""
+    rng = np.random.default_rng(5)
+    n = 384
+    q, k, v = _inputs(rng, 2, n)
+    rows, fb = 2 * (n // 128), n // 4
+    perm = np.stack([rng.permutation(fb) for _ in range(rows)]).astype(np.int32)
+    a_ids, b_ids = perm[:, :40], perm[:, 40:72]
+    a_w = (rng.random((rows, 40)) * 3).astype(np.float32)
+    b_w = np.zeros((rows, 32), np.float32)
+    oa, la = oracle_mod.prefill(q, k, v, a_ids, a_w)
+    ob, lb = oracle_mod.prefill(q, k, v, b_ids, b_w)
+    om, lm = oracle_mod.merge_states(oa, la, ob, lb)
+    ou, lu = oracle_mod.prefill(q, k, v, np.concatenate([a_ids, b_ids], 1), np.concatenate([a_w, b_w], 1))
+    np.testing.assert_allclose(om, ou, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(lm, lu, rtol=1e-6, atol=1e-5)
+    # a state merged with an empty one (lse -inf) is unchanged
+    o2, l2 = oracle_mod.merge_states(oa, la, ob, np.full_like(lb, -np.inf))
+    np.testing.assert_allclose(o2, oa, rtol=1e-12, atol=0)
+    np.testing.assert_allclose(l2, la, rtol=1e-12, atol=0)
