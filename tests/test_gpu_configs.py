@@ -1,0 +1,115 @@
+"""Full-length heads of the HunyuanVideo (c3) and cube-layout (c4) workloads on
+the GPU, end to end through the public API.
+
+c3 (HunyuanVideo-13B 720p, 129 frames): 118,800 video tokens and 256 prompt
+tokens, 71 sample pages, so each row samples 2,272 of 29,700 KV4 blocks (SIP's
+global-memory path). One head runs ``hunyuan_attention`` on a sparse step
+(reference: ab_attention/video.py:129-151). The oracle checks the plan
+(bit-exact SIP on the GPU's own IBCS scores and the schedule's uniforms) on a
+subset of rows, then a few video rows and both prompt rows against exact fp64
+attention: video rows over the plan plus every prompt block, prompt rows over
+all keys.
+
+c4 (Wan2.1-14B 720p, cube layout): one head with its tokens in 4x4x4-cube
+order (the permutation of video.py:97-105, applied to Q/K/V as the reference's
+hooks apply it to the hidden states) through ``ab_attention``, checked the same
+way; the inverse permutation then restores raster order.
+
+Bars: SIP bit-exact; output max-abs 2e-2 per row and rel-L2 1e-2 (bf16).
+"""
+import numpy as np
+import pytest
+import torch
+
+from ab_attention import _C, apply_plan, build_plan
+from ab_attention.synthetic import CONFIGS, make_qkv
+from ab_attention.video import VideoAttention, cube_order, hunyuan_attention
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, REL_L2 = 2e-2, 1e-2
+
+
+def _f32(t):
+    return t.float().cpu().numpy()
+
+
+def _check_rows(got, ref, rows, n):
+    """got/ref [n, 128]; compare the queries of the given 128-query rows."""
+    for r in rows:
+        lo, hi = r * 128, min(n, r * 128 + 128)
+        g, e = np.asarray(got[lo:hi], np.float64), np.asarray(ref[lo:hi], np.float64)
+        err = np.abs(g - e).max()
+        assert err <= MAX_ABS, (r, err)
+        rel = np.linalg.norm(g - e) / np.linalg.norm(e)
+        assert rel <= REL_L2, (r, rel)
+
+
+def _check_sip(oracle_mod, q, k, plan, seed, rows):
+    """The plan's rows equal the oracle's SIP on the GPU's scores and uniforms."""
+    n_rows = plan.descriptor.shape[0]
+    samples = plan.descriptor.shape[1] * plan.descriptor.shape[2]
+    scores = _C.ibcs(q, k)
+    offsets = torch.rand(n_rows, device=q.device, generator=torch.Generator(q.device).manual_seed(seed))
+    idx = torch.as_tensor(rows, dtype=torch.long, device=q.device)
+    ids_o, w_o = oracle_mod.sip(scores[idx].cpu().numpy(), offsets[idx].cpu().numpy(), samples)
+    ids_g = plan.descriptor.reshape(n_rows, samples)[idx].cpu().numpy()
+    w_g = plan.log_weights.reshape(n_rows, samples)[idx].cpu().numpy()
+    assert np.array_equal(ids_g, ids_o)
+    assert np.array_equal(w_g.view(np.uint32), w_o.view(np.uint32))
+
+
+def test_c3_hunyuan_head(oracle_mod):
+    cfg = CONFIGS[3]
+    video, prompt = cfg.video_tokens, cfg.text_tokens
+    print(f"c3 head 5: {video} video + {prompt} prompt tokens, P={cfg.sample_pages}", flush=True)
+    q, k, v = make_qkv(cfg, heads=[5], device="cuda", dtype=torch.bfloat16)
+    n = q.shape[2]
+    sched = VideoAttention(cfg.sample_pages)
+    sched.step = 11
+    out = hunyuan_attention(sched, 1, q, k, v, video, prompt)
+    torch.cuda.synchronize()
+    assert out.shape == q.shape and out.dtype == torch.bfloat16
+    anchor, plan = sched.plans[1]
+    seed = 42 + 1 * 1_000_003 + anchor * 97
+    rows = plan.descriptor.shape[0]
+    assert rows == -(-video // 128) and plan.descriptor.shape[1] == cfg.sample_pages
+    keep = np.array([0, 1, rows // 2, rows - 2, rows - 1])
+    _check_sip(oracle_mod, q[:, :, :video].contiguous(), k[:, :, :video].contiguous(), plan, seed, keep)
+
+    qf, kf, vf = (_f32(t).reshape(1, n, 128) for t in (q, k, v))
+    got = _f32(out).reshape(n, 128)
+    # video rows: sampled blocks at their SIP weights, then every prompt block at weight 0
+    text_ids = np.arange(video // 4, (video + prompt) // 4, dtype=np.int32)
+    ids = np.concatenate([plan.descriptor.reshape(rows, -1).cpu().numpy(), np.tile(text_ids, (rows, 1))], 1)
+    w = np.concatenate([plan.log_weights.reshape(rows, -1).cpu().numpy(), np.zeros((rows, text_ids.size), np.float32)], 1)
+    ref, _ = oracle_mod.prefill(qf[:, :video], kf, vf, ids, w, rows=keep)
+    _check_rows(got[:video], ref[0], keep, video)
+    # prompt rows: exact attention over every key
+    all_ids = np.tile(np.arange((video + prompt) // 4, dtype=np.int32), (2, 1))
+    ref_p, _ = oracle_mod.prefill(qf[:, video:], kf, vf, all_ids, np.zeros(all_ids.shape, np.float32))
+    _check_rows(got[video:], ref_p[0], [0, 1], prompt)
+
+
+def test_c4_cube_layout_head(oracle_mod):
+    cfg = CONFIGS[4]
+    print(f"c4 head 3 in cube order, grid {cfg.grid}", flush=True)
+    q, k, v = (t[:1].contiguous() for t in make_qkv(cfg, heads=[3], device="cuda", dtype=torch.bfloat16))
+    n = q.shape[2]
+    order, inverse = cube_order(cfg.grid)
+    order, inverse = order.cuda(), inverse.cuda()
+    qc, kc, vc = (t.index_select(2, order) for t in (q, k, v))
+    seed = 7
+    plan = build_plan(qc, kc, sample_pages=cfg.sample_pages, seed=seed)
+    out_cube = apply_plan(qc, kc, vc, plan)
+    out = out_cube.index_select(2, inverse)
+    torch.cuda.synchronize()
+    rows = plan.descriptor.shape[0]
+    keep = np.array([0, 3, rows // 2, rows - 1])
+    _check_sip(oracle_mod, qc, kc, plan, seed, keep)
+    ids = plan.descriptor.reshape(rows, -1).cpu().numpy()
+    w = plan.log_weights.reshape(rows, -1).cpu().numpy()
+    ref, _ = oracle_mod.prefill(*(_f32(t).reshape(1, n, 128) for t in (qc, kc, vc)), ids, w, rows=keep)
+    _check_rows(_f32(out_cube).reshape(n, 128), ref[0], keep, n)
+    # raster order restored: token i of `out` is cube position inverse[i]
+    assert torch.equal(out.index_select(2, order), out_cube)
