@@ -11,13 +11,18 @@
 //
 // Kernel shape: one workgroup (4 waves) per row, two workgroups per CU; wave
 // w owns queries 32w..32w+31. The row's pages are streamed in tiles of 8 KV4
-// blocks (32 keys) through a ring of kStages LDS stages that the hardware
-// fills directly from global memory (global_load_lds_dwordx4: no staging
-// registers, kStages-1 tiles in flight per workgroup). Each wave moves one
-// quarter of every tile and waits only for its own tile-t transfers
-// (s_waitcnt vmcnt) before the workgroup barrier that publishes tile t.
-// The page ids and weights of the row reach LDS the same way, 64 tiles at a
-// time, so the loop issues no other global or scalar loads.
+// blocks (32 keys) through two rings of 4 LDS stages, one for K and one for
+// V, that the hardware fills directly from global memory
+// (global_load_lds_dwordx4: no staging registers). Each wave moves one
+// quarter of every tile and waits only for its own transfers (s_waitcnt
+// vmcnt) before the workgroup barrier that publishes them; every transfer
+// has three steps to land. The page ids and weights of the row reach LDS the
+// same way, 64 tiles at a time, so the loop issues no other global or scalar
+// loads; ids and weights are read from LDS one step before their use.
+// The loop is software pipelined (see step below): each step issues 16 MFMAs
+// of two different tiles and places the softmax VALU work, the LDS operand
+// reads and the transfers of other tiles between them, so the MFMA pipe of
+// each SIMD is fed while LDS and the vector memory path are busy.
 //   S^T = K Q^T  : v_mfma_f32_32x32x16_bf16, A = K rows from LDS, B = Q in VGPRs
 //                  -> each lane holds one query and 16 keys, in 4-key groups
 //                     that are exactly one KV4 block.
@@ -38,17 +43,18 @@ namespace ab {
 namespace {
 
 constexpr int kPfThreads = 256;
-constexpr int kStages = 4;
+constexpr int kRing = 4;                                       // stages per ring (K and V)
 constexpr int kTilePages = 8;                                  // KV4 blocks per tile
 constexpr int kPageBytes = kKvBlock * kHeadDim * 2;            // 1 KiB of K (or V)
-constexpr int kHalfBytes = kTilePages * kPageBytes;            // K (or V) of one tile
-constexpr int kStageBytes = 2 * kHalfBytes;                    // 16 KiB
+constexpr int kTileBytes = kTilePages * kPageBytes;            // 8 KiB: K (or V) of one tile
+constexpr int kKRing = 0;
+constexpr int kVRing = kRing * kTileBytes;
 constexpr int kBatchTiles = 64;                                // ids/weights per LDS batch
 constexpr int kBatchBytes = kBatchTiles * kTilePages * 4;      // 2 KiB
-constexpr int kIdsOffset = kStages * kStageBytes;              // 2 batch buffers of ids
+constexpr int kIdsOffset = 2 * kRing * kTileBytes;             // 2 batch buffers of ids
 constexpr int kWeightsOffset = kIdsOffset + 2 * kBatchBytes;   // 2 batch buffers of weights
-constexpr int kLdsBytes = kWeightsOffset + 2 * kBatchBytes;
-constexpr int kDmaPerTile = 4;                                 // transfers per wave per tile
+constexpr int kLdsBytes = kWeightsOffset + 2 * kBatchBytes;    // 72 KiB
+constexpr int kGroupOps = 4;                                   // transfers per wave per step
 // Largest p = 2^(y) allowed before the running reference is moved.
 constexpr float kSlack = 8.0f;
 
@@ -146,7 +152,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
         }
     };
 
-    // Tile transfers of this wave: pages 2w and 2w+1 of the tile, K and V.
+    // Transfers of this wave: pages 2w and 2w+1 of a K tile and of a V tile.
     // Source offsets inside a page (1 KiB = 4 keys x 256 B) for lane j:
     //   K: key r = j/16 at LDS chunk position j%16 holds chunk pos ^ (key & 15);
     //   V: block m = j/8, row slot (j/2)%4 holds key slot ^ ((m>>1)&3), dims 16m + 8(j%2).
@@ -161,17 +167,32 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
         const int m = lane >> 3, sl = (lane >> 1) & 3, h = lane & 1;
         return uint32_t((sl ^ ((m >> 1) & 3)) * 16 + 2 * m + h) * 16u;
     }();
-    auto issue_tile = [&](int u) {
-        const int* idp = reinterpret_cast<const int*>(smem + kIdsOffset + ((u / kBatchTiles) & 1) * kBatchBytes) +
-                         (u % kBatchTiles) * kTilePages + 2 * wave;
-        // Clamp so a malformed plan can never address outside the head.
-        const uint32_t j0 = uint32_t(min(max(idp[0], 0), fb - 1));
-        const uint32_t j1 = uint32_t(min(max(idp[1], 0), fb - 1));
-        const uint32_t st = lds0 + (u % kStages) * kStageBytes + 2 * wave * kPageBytes;
-        dma16(kbase, j0 * kPageBytes + k_src[0], st);
-        dma16(kbase, j1 * kPageBytes + k_src[1], st + kPageBytes);
-        dma16(vbase, j0 * kPageBytes + v_src, st + kHalfBytes);
-        dma16(vbase, j1 * kPageBytes + v_src, st + kHalfBytes + kPageBytes);
+    // This wave's two page ids of tile u, clamped into the head (a malformed
+    // plan can never address outside it); tiles past the row's end read its
+    // last tile (their transfers only keep the per-step count uniform).
+    auto load_ids = [&](int u) {
+        const int uc = min(u, tiles - 1);
+        const u32x2 raw = *reinterpret_cast<const u32x2*>(smem + kIdsOffset + ((uc / kBatchTiles) & 1) * kBatchBytes +
+                                                          ((uc % kBatchTiles) * kTilePages + 2 * wave) * 4);
+        const u32x2 c = {uint32_t(min(max(static_cast<int>(raw[0]), 0), fb - 1)),
+                         uint32_t(min(max(static_cast<int>(raw[1]), 0), fb - 1))};
+        return c;
+    };
+    auto dma_k = [&](int u, uint32_t id, int e) {
+        dma16(kbase, id * kPageBytes + k_src[e], lds0 + kKRing + (u % kRing) * kTileBytes + (2 * wave + e) * kPageBytes);
+    };
+    auto dma_v = [&](int u, uint32_t id, int e) {
+        dma16(vbase, id * kPageBytes + v_src, lds0 + kVRing + (u % kRing) * kTileBytes + (2 * wave + e) * kPageBytes);
+    };
+    // The four block weights of this lane's keys in tile u: lane register r
+    // holds key 8*(r/4) + 4*half + r%4, i.e. page 2(r/4) + half.
+    auto load_weights = [&](int u, float (&wv)[4]) {
+        const int uc = min(u, tiles - 1);
+        const float* ws = reinterpret_cast<const float*>(smem + kWeightsOffset +
+                                                         ((uc / kBatchTiles) & 1) * kBatchBytes) +
+                          (uc % kBatchTiles) * kTilePages;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) wv[g] = ws[2 * g + half];
     };
 
     // Operand-read offsets of this lane (stage-relative).
@@ -182,9 +203,22 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
     {
         const int gd = (lane >> 4) & 1, r = (lane >> 2) & 3, q4 = lane & 3;
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
-            v_off[dt] = kHalfBytes + half * 1024 + (2 * dt + gd) * 128 + 32 * (r ^ dt) + 8 * q4;
+        for (int dt = 0; dt < 4; ++dt) v_off[dt] = half * 1024 + (2 * dt + gd) * 128 + 32 * (r ^ dt) + 8 * q4;
     }
+    auto read_k = [&](int u, int j) {
+        return *reinterpret_cast<const u32x4*>(smem + kKRing + (u % kRing) * kTileBytes + k_off[j]);
+    };
+    // PV A operand j of tile u: V^T for k-step j/4, dims 32(j%4) .. +31. MFMA
+    // k-index 8*half + 4t + r of k-step ks is key r of tile page 4*ks + 2t +
+    // half, on both operands. Lane (group g = lane/16, i = lane%16) does two
+    // transposing reads; the source lane 4r + q addresses key r of that page,
+    // dims 32dt + 16(g%2) + 4q .. +3, so lane i receives dim 32dt + 16(g%2) + i.
+    auto read_v = [&](int u, int j) {
+        const unsigned char* p0 = smem + kVRing + (u % kRing) * kTileBytes + v_off[j & 3] + (j >> 2) * 4096;
+        const i16x4 lo = lds_read_tr16(p0);
+        const i16x4 hi = lds_read_tr16(p0 + 2048);
+        return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    };
 
     f32x16 o_acc[4];
 #pragma unroll
@@ -193,62 +227,36 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
         for (int r = 0; r < 16; ++r) o_acc[dt][r] = 0.f;
     float m_run = 0.f, l_run = 0.f;  // reference set by the first tile
 
-    // Prologue: the first batch of ids/weights (this also completes the Q
-    // loads), then tiles 0 .. kStages-2.
-    if (wave == 0) issue_batch(0);
-    wait_and_barrier<0>();
-    for (int u = 0; u < kStages - 1 && u < tiles; ++u) issue_tile(u);
-
-    for (int tile = 0; tile < tiles; ++tile) {
-        // This wave's transfers for tile t are done once at most 4g newer ones
-        // (tiles t+1 .. t+g) are outstanding; the barrier then publishes the
-        // whole tile and retires every read of the stage refilled below.
-        const int ahead = tiles - 1 - tile;
-        if (ahead >= kStages - 2)
-            wait_and_barrier<kDmaPerTile * (kStages - 2)>();
-        else if (ahead == 1)
-            wait_and_barrier<kDmaPerTile>();
-        else
-            wait_and_barrier<0>();
-        if (tile + kStages - 1 < tiles) issue_tile(tile + kStages - 1);
-        if (wave == 0 && tile % kBatchTiles == kBatchTiles / 2 && (tile / kBatchTiles + 1) * kBatchTiles < tiles)
-            issue_batch(tile / kBatchTiles + 1);
-
-        const unsigned char* st = smem + (tile % kStages) * kStageBytes;
-        const float* ws = reinterpret_cast<const float*>(smem + kWeightsOffset +
-                                                         ((tile / kBatchTiles) & 1) * kBatchBytes) +
-                          (tile % kBatchTiles) * kTilePages;
-
-        // S^T of the tile's 32 keys.
-        f32x16 sacc;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            const bf16x8 a = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(st + k_off[s]));
-            sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bq[s], sacc, 0, 0, 0);
+    // Step t works on three tiles at once, so that every MFMA of the wave has
+    // independent VALU and LDS work beside it. Entering step t, sc holds the
+    // logits y = s*log2(e)/sqrt(d) + (w - m_run) of S(t) and mx their maximum
+    // over this lane's keys.
+    //   phase A: S(t+1) = K(t+1) Q^T (K(t+1) already in registers), beside
+    //            p = 2^y of S(t), the reads of V(t) and this step's four
+    //            transfers;
+    //   phase B: O += V(t)^T P(t)^T, beside the logits of S(t+1) and the
+    //            reads of K(t+2) for the next step.
+    // Lazy rescaling: the reference moves only when a tile maximum exceeds it
+    // by more than kSlack (so p <= 2^kSlack), decided per wave at the start of
+    // the step that exponentiates the tile.
+    // Rings: K(u) is read in step u-2 and V(u) in step u. Step t transfers
+    // K(t+5) into the stage of K(t+1) and V(t+3) into the stage of V(t-1),
+    // both read in step t-1; the barrier at the top of step t retires those
+    // reads and publishes K(t+2) and V(t) (transferred in step t-3), so every
+    // transfer has three steps. Transfers past the row's end keep the count
+    // uniform (4 per wave per step) and land in stages nobody reads again.
+    auto step = [&](int t, f32x16& sc, f32x16& sn, float& mx, u32x4 (&ka)[8], float (&wn)[4], u32x2& idk,
+                    u32x2& idv) {
+        wait_and_barrier<2 * kGroupOps>();
+        if (wave == 0 && t % kBatchTiles == kBatchTiles / 2 && (t / kBatchTiles + 1) * kBatchTiles < tiles)
+            issue_batch(t / kBatchTiles + 1);
+        {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+            mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
         }
-
-        // Logits in base 2 with the block weights; lane register r holds key
-        // 8*(r/4) + 4*half + r%4 of the tile, i.e. page 2(r/4) + half.
-        // Scores are kept relative to the running reference m_run:
-        //   y = s * log2(e)/sqrt(d) + (w - m_run),   p = 2^y.
-        float wm[4];
-#pragma unroll
-        for (int g = 0; g < 4; ++g) wm[g] = ws[2 * g + half] - m_run;
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const float y = __builtin_fmaf(sacc[r], scale_log2, wm[r >> 2]);
-            sacc[r] = y;
-            tmax = fmaxf(tmax, y);
-        }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        // Lazy rescaling: the reference moves only when the tile maximum exceeds
-        // it by more than kSlack (so p <= 2^kSlack); the branch is wave-uniform.
-        const bool grow = tile == 0 || tmax > kSlack;
+        const bool grow = t == 0 || mx > kSlack;
         if (__any(grow)) {
-            const float shift = grow ? tmax : 0.f;
+            const float shift = grow ? mx : 0.f;
             const float alpha = fast_exp2(-shift);
             m_run += shift;
             l_run *= alpha;
@@ -257,44 +265,123 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
 #pragma unroll
                 for (int r = 0; r < 16; ++r) o_acc[dt][r] *= alpha;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) sacc[r] -= shift;
+            for (int r = 0; r < 16; ++r) sc[r] -= shift;
         }
-        float psum = 0.f;
         uint32_t pw[4][2];
+        float psum = 0.f;
+        bf16x8 va[8];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            float p[4];
+        for (int r = 0; r < 16; ++r) sn[r] = 0.f;
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                p[i] = fast_exp2(sacc[4 * g + i]);
-                psum += p[i];
-            }
-            pw[g][0] = pack_bf16(p[0], p[1]);
-            pw[g][1] = pack_bf16(p[2], p[3]);
+        for (int j = 0; j < 8; ++j) {
+            sn = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ka[j]), bq[j], sn, 0, 0, 0);
+            const float p0 = fast_exp2(sc[2 * j]), p1 = fast_exp2(sc[2 * j + 1]);
+            psum += p0;
+            psum += p1;
+            pw[j >> 1][j & 1] = pack_bf16(p0, p1);
+            va[j] = read_v(t, j);
+            if (j == 1) dma_k(t + 5, idk[0], 0);
+            if (j == 3) dma_k(t + 5, idk[1], 1);
+            if (j == 5) dma_v(t + 3, idv[0], 0);
+            if (j == 7) dma_v(t + 3, idv[1], 1);
+            if (j == 2) load_weights(t + 1, wn);
+            __builtin_amdgcn_sched_barrier(0);
         }
         l_run += psum;
-
-        // O^T += V^T P^T over 2 k-steps of 16 keys. MFMA k-index 8*half + 4t + r
-        // of k-step ks is key r of tile page 4*ks + 2t + half, on both operands.
-        // A operand of lane (group g = lane/16, i = lane%16): two transposing
-        // reads; the source lane 4r + q addresses key r of that page, dims
-        // 32dt + 16(g%2) + 4q .. +3, so lane i receives dim 32dt + 16(g%2) + i.
+        float wm[4];
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
+        for (int g = 0; g < 4; ++g) wm[g] = wn[g] - m_run;
+        mx = -INFINITY;
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int ks = j >> 2;
             const u32x4 bw = {pw[2 * ks][0], pw[2 * ks][1], pw[2 * ks + 1][0], pw[2 * ks + 1][1]};
-            const bf16x8 b = __builtin_bit_cast(bf16x8, bw);
+            o_acc[j & 3] =
+                __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[j], __builtin_bit_cast(bf16x8, bw), o_acc[j & 3], 0, 0, 0);
+            ka[j] = read_k(t + 2, j);
+            const float y0 = __builtin_fmaf(sn[2 * j], scale_log2, wm[j >> 1]);
+            const float y1 = __builtin_fmaf(sn[2 * j + 1], scale_log2, wm[j >> 1]);
+            sn[2 * j] = y0;
+            sn[2 * j + 1] = y1;
+            mx = fmaxf(mx, fmaxf(y0, y1));
+            if (j == 6) idk = load_ids(t + 6);
+            if (j == 7) idv = load_ids(t + 4);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // Prologue: batch 0 of ids/weights (this also completes the Q loads);
+    // K(0..3) and V(0..2); S(0) and K(1) into registers once K(0) and K(1)
+    // are in; K(4) goes into K(0)'s stage only after every wave has read it.
+    // The last eight transfers before step 0 are then K(3), V(1), V(2), K(4),
+    // as step 0's wait expects.
+    if (wave == 0) issue_batch(0);
+    wait_and_barrier<0>();
+    {
 #pragma unroll
-            for (int dt = 0; dt < 4; ++dt) {
-                const unsigned char* p0 = st + v_off[dt] + ks * 4096;
-                const i16x4 lo = lds_read_tr16(p0);
-                const i16x4 hi = lds_read_tr16(p0 + 2048);
-                const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-                o_acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, o_acc[dt], 0, 0, 0);
-            }
+        for (int u = 0; u < 3; ++u) {
+            const u32x2 ik = load_ids(u);
+            dma_k(u, ik[0], 0);
+            dma_k(u, ik[1], 1);
+        }
+        const u32x2 iv0 = load_ids(0);
+        dma_v(0, iv0[0], 0);
+        dma_v(0, iv0[1], 1);
+        const u32x2 ik3 = load_ids(3);
+        dma_k(3, ik3[0], 0);
+        dma_k(3, ik3[1], 1);
+        const u32x2 iv1 = load_ids(1), iv2 = load_ids(2);
+        dma_v(1, iv1[0], 0);
+        dma_v(1, iv1[1], 1);
+        dma_v(2, iv2[0], 0);
+        dma_v(2, iv2[1], 1);
+    }
+    const u32x2 ik4 = load_ids(4);
+    u32x2 idk = load_ids(5), idv = load_ids(3);
+    wait_and_barrier<10>();  // K(0), K(1) in; 10 newer transfers may be in flight
+    f32x16 s0, s1;
+    u32x4 ka[8];
+    {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ka[j] = read_k(0, j);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s0[r] = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ka[j]), bq[j], s0, 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ka[j] = read_k(1, j);
+    }
+    wait_and_barrier<63>();  // every wave's reads of K(0) are done (no transfer wait)
+    dma_k(4, ik4[0], 0);
+    dma_k(4, ik4[1], 1);
+    // Logits of S(0).
+    float w0[4], mx;
+    load_weights(0, w0);
+    {
+        float wm[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) wm[g] = w0[g] - m_run;
+        mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            s0[r] = __builtin_fmaf(s0[r], scale_log2, wm[r >> 2]);
+            mx = fmaxf(mx, s0[r]);
         }
     }
+    int t = 0;
+    for (; t + 1 < tiles; t += 2) {
+        step(t, s0, s1, mx, ka, w0, idk, idv);
+        step(t + 1, s1, s0, mx, ka, w0, idk, idv);
+    }
+    if (t < tiles) step(t, s0, s1, mx, ka, w0, idk, idv);
+    // No transfer may still be landing when the workgroup's LDS is released.
+    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0)
 
-    const float l_tot = l_run + __shfl_xor(l_run, 32);
+    const auto lsw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
+    const float l_tot = __uint_as_float(lsw[0]) + __uint_as_float(lsw[1]);
     if (valid_q) {
         const float inv = 1.0f / l_tot;
         uint16_t* orow = out + (bh * n + token) * kHeadDim;
@@ -378,3 +465,4 @@ int launch_prefill(const void* q, const void* k, const void* v, int64_t bh, int6
 }
 
 }  // namespace ab
+
