@@ -54,6 +54,16 @@ __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_lo
 
 __device__ __forceinline__ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS accesses
+// (lgkmcnt(0)) but leaves its outstanding global loads in flight. HIP's
+// __syncthreads() also waits for every outstanding global load (vmcnt(0)),
+// which would drain a prefetch issued before the barrier.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
+    asm volatile("s_barrier" ::: "memory");
+}
+
 }  // namespace ab
 
 // Error reporting shared by every C-ABI entry point (api.hip).

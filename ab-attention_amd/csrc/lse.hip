@@ -81,14 +81,6 @@ __device__ __forceinline__ void wait_vmcnt() {
     asm volatile("" ::: "memory");
 }
 
-// Workgroup barrier for LDS traffic only: waits for this wave's LDS accesses
-// (lgkmcnt(0)) but leaves its outstanding global transfers in flight.
-__device__ __forceinline__ void lds_barrier() {
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
-    asm volatile("s_barrier" ::: "memory");
-}
-
 __device__ __forceinline__ void combine_pair(float& m, float& d, float om, float od) {
     const float nm = fmaxf(m, om);
     d = d * fast_exp2(m - nm) + od * fast_exp2(om - nm);

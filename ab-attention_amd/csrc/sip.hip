@@ -170,7 +170,7 @@ __device__ __forceinline__ void sip_row(R& rv, double sum, double mx, double* pr
                 sh.group_max[t >> 5] = mx;
             }
         }
-        __syncthreads();
+        lds_barrier();
         if (t == 0) {
             double total = sh.part[0], maximum = sh.group_max[0];
             for (int w = 1; w < kSipThreads / 32; ++w) {
@@ -182,7 +182,7 @@ __device__ __forceinline__ void sip_row(R& rv, double sum, double mx, double* pr
             sh.pass = maximum * sc >= 1.0;
             sh.added = 0;
         }
-        __syncthreads();
+        lds_barrier();
         scale = sh.scale;
         if (sh.pass) {
             int count = 0;
@@ -193,11 +193,11 @@ __device__ __forceinline__ void sip_row(R& rv, double sum, double mx, double* pr
                 }
             if (count) atomicAdd(&sh.added, count);
         }
-        __syncthreads();
+        lds_barrier();
         const int added = sh.added;
         certainty += added;
         rv.set_any_certain(certainty != 0);
-        __syncthreads();
+        lds_barrier();
         if (added == 0) break;
     }
 
@@ -205,12 +205,12 @@ __device__ __forceinline__ void sip_row(R& rv, double sum, double mx, double* pr
     int last = pop - 1;
     if (certainty != 0) {
         if (t == 0) sh.last = -1;
-        __syncthreads();
+        lds_barrier();
         int mine = -1;
         for (int i = t; i < pop; i += kSipWorkers)
             if (!rv.certain(i)) mine = i;
         if (mine >= 0) atomicMax(&sh.last, mine);
-        __syncthreads();
+        lds_barrier();
         last = sh.last;
     }
 
@@ -233,7 +233,7 @@ __device__ __forceinline__ void sip_row(R& rv, double sum, double mx, double* pr
             }
             if ((t & 63) == 63) sh.wave_count[t >> 6] = inc;
         }
-        __syncthreads();
+        lds_barrier();
         if (logical) {
             int slot = inc - count;
             for (int w = 0; w < (t >> 6); ++w) slot += sh.wave_count[w];
@@ -243,7 +243,7 @@ __device__ __forceinline__ void sip_row(R& rv, double sum, double mx, double* pr
                     out_w[slot++] = 0.f;
                 }
         }
-        __syncthreads();
+        lds_barrier();
     }
 
     // Chunk masses and their CUB-ordered exclusive scan (sip.cu:126-130).
@@ -264,7 +264,7 @@ __device__ __forceinline__ void sip_row(R& rv, double sum, double mx, double* pr
         }
         sh.part[t] = chunk_mass;
     }
-    __syncthreads();
+    lds_barrier();
     if (t < 32) {
         double seg = sh.part[8 * t];
 #pragma unroll
@@ -285,7 +285,7 @@ __device__ __forceinline__ void sip_row(R& rv, double sum, double mx, double* pr
             ex = ex + in;
         }
     }
-    __syncthreads();
+    lds_barrier();
 
     // Bucket prefixes (sip.cu:131-142).
     const int residuals = samples - certainty;
@@ -306,7 +306,7 @@ __device__ __forceinline__ void sip_row(R& rv, double sum, double mx, double* pr
             }
         }
     }
-    __syncthreads();
+    lds_barrier();
 
     // Systematic draws (sip.cu:144-166). Each thread runs up to kDraws
     // independent searches in lockstep (their LDS reads overlap); every search
@@ -361,7 +361,7 @@ __device__ __forceinline__ void sip_row(R& rv, double sum, double mx, double* pr
             weight[d] = static_cast<float>(-log2(rv.weight_mass(sel) * scale));
         }
         if (round + 1 == rounds) {
-            __syncthreads();
+            lds_barrier();
             stage_next();
         }
 #pragma unroll
@@ -374,7 +374,7 @@ __device__ __forceinline__ void sip_row(R& rv, double sum, double mx, double* pr
         }
     }
     if (rounds == 0) {
-        __syncthreads();
+        lds_barrier();
         stage_next();
     }
 }
@@ -394,12 +394,16 @@ __global__ __launch_bounds__(kSipWorkers) void sip_lds_kernel(
     float* values = reinterpret_cast<float*>(smem + sip_values_offset(buckets));
 
     float next[kPer];
+    // Load k of a row reads element t + 1024k through a wave-uniform base
+    // pointer, so no per-load offsets stay live across the row (spilled
+    // offsets would be reloaded from scratch, and each reload's wait would
+    // also wait for the prefetch loads already issued).
     auto prefetch = [&](int64_t r) {
         const float* in = masses + r * int64_t(pop);
 #pragma unroll
         for (int k = 0; k < kPer; ++k) {
-            const int i = t + k * kSipWorkers;
-            next[k] = i < pop ? in[i] : 0.0f;
+            const float* base = in + k * kSipWorkers;
+            next[k] = t + k * kSipWorkers < pop ? base[t] : 0.0f;
         }
     };
     auto stage = [&] {
@@ -417,7 +421,7 @@ __global__ __launch_bounds__(kSipWorkers) void sip_lds_kernel(
     for (; row < rows; row += gridDim.x) {
         const int64_t following = row + gridDim.x;
         if (following < rows) prefetch(following);
-        __syncthreads();  // this row is staged
+        lds_barrier();  // this row is staged
         LdsRow rv{values};
         double sum = 0.0, mx = 0.0;
         if (t < kSipThreads) strided_partials(rv, pop, sum, mx);
@@ -440,7 +444,7 @@ __global__ __launch_bounds__(kSipWorkers) void sip_global_kernel(
     double* prefix = reinterpret_cast<double*>(smem);
     GlobalRow rv{masses + row * int64_t(pop), reinterpret_cast<uint32_t*>(prefix + buckets + 1), false, pop - 1};
     for (int w = t; w < (pop + 31) / 32; w += kSipWorkers) rv.marks[w] = 0u;
-    __syncthreads();
+    lds_barrier();
     double sum = 0.0, mx = 0.0;
     if (t < kSipThreads) strided_partials(rv, pop, sum, mx);
     sip_row(rv, sum, mx, prefix, sh, offsets[row], ids + row * int64_t(samples), logw + row * int64_t(samples),
