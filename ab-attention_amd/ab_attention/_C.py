@@ -52,6 +52,27 @@ def ibcs(q: torch.Tensor, k: torch.Tensor) -> torch.Tensor:
     return scores
 
 
+def ibcs_ordered(q: torch.Tensor, k: torch.Tensor, order: torch.Tensor) -> torch.Tensor:
+    """ibcs of q, k with their tokens taken in the order ``order`` (int32 [tokens],
+    a permutation: position t is stored token order[t]), without permuting them.
+    Same checks and result layout as ``ibcs`` of the permuted tensors."""
+    _require(q.is_contiguous() and k.is_contiguous(), "q and k must be contiguous")
+    _require(q.is_cuda and k.is_cuda, "q and k must be CUDA tensors")
+    _require(order.dtype == torch.int32 and order.is_contiguous() and order.device == q.device
+             and order.shape == (q.shape[2],), "order must be int32 [tokens] on the q device")
+    batch, heads, tokens = q.shape[0], q.shape[1], q.shape[2]
+    batch_heads = batch * heads
+    rows = batch_heads * -(-tokens // QUERY_BLOCK)
+    lib = _lib.load()
+    with torch.cuda.device(q.device):
+        ws_bytes = lib.ab_ibcs_workspace_bytes(batch_heads, tokens)
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+        scores = torch.empty((rows, tokens // KV_BLOCK), dtype=torch.float32, device=q.device)
+        _lib.check(lib.ab_ibcs_ordered(_lib.ptr(q), _lib.ptr(k), _lib.ptr(order), batch_heads, tokens,
+                                       _lib.ptr(workspace), ws_bytes, _lib.ptr(scores), _lib.stream(q.device)))
+    return scores
+
+
 def sip(scores: torch.Tensor, offsets: torch.Tensor, ids: torch.Tensor, logs: torch.Tensor) -> None:
     """SIP sampling into the caller's ``ids``/``logs`` slices (csrc/sip.cu:170-199)."""
     _require(scores.is_cuda and offsets.device == scores.device and ids.device == scores.device

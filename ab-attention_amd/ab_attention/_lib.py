@@ -34,6 +34,9 @@ SIGNATURES = {
     "ab_paged_prefill": (ctypes.c_int, [_P, _P, _P, _I64, _I64, _P, _P, _I64, _P, _P, _P]),
     "ab_paged_prefill_kv": (ctypes.c_int, [_P, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _P, _P, _P]),
     "ab_merge_states": (ctypes.c_int, [_P, _P, _P, _P, _I64, _P, _P, _P]),
+    "ab_ibcs_ordered": (ctypes.c_int, [_P, _P, _P, _I64, _I64, _P, _SZ, _P, _P]),
+    "ab_remap_ids": (ctypes.c_int, [_P, _I64, _P, _I64, _P, _P]),
+    "ab_paged_prefill_ordered": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _P, _P, _I64, _P, _P, _P]),
 }
 
 ABI_VERSION = 1

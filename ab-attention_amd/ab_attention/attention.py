@@ -53,6 +53,13 @@ def build_plan(q, k, *, sample_pages=64, seed=42):
     Returns a ``SamplePlan`` with both tensors shaped [rows, pages, 32].
     (Reference: attention.py:26-82.)
     """
+    from . import _C as ops
+
+    return _build_plan(q, k, sample_pages, seed, ops.ibcs)
+
+
+def _build_plan(q, k, sample_pages, seed, ibcs):
+    """build_plan with the scoring step ``ibcs(q_chunk, k_chunk) -> scores``."""
     sample_pages = int(sample_pages)
     if q.ndim != 4 or q.shape != k.shape or q.shape[2] % 4:
         raise ValueError("Q/K must match [B,H,N,D] with N divisible by 4")
@@ -80,7 +87,7 @@ def build_plan(q, k, *, sample_pages=64, seed=42):
     for start in range(0, batch_heads, heads_per_chunk):
         stop = min(batch_heads, start + heads_per_chunk)
         first, last = start * q_blocks, stop * q_blocks
-        scores = ops.ibcs(
+        scores = ibcs(
             flat_q[start:stop].unsqueeze(0).contiguous(),
             flat_k[start:stop].unsqueeze(0).contiguous(),
         )

@@ -27,6 +27,20 @@ _QUERY_BLOCK = 128
 _PAGE_SIZE = 4
 
 
+def check_prefill_inputs(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
+    """paged_attention's Q/K/V checks (reference: flashinfer_backend.py:176-186)."""
+    if q.ndim != 4 or q.shape != k.shape or q.shape != v.shape:
+        raise ValueError("Q/K/V must have the same [B,H,N,D] shape")
+    if q.device != k.device or q.device != v.device:
+        raise ValueError("Q/K/V must be on the same CUDA device")
+    if q.device.type != "cuda":
+        raise ValueError("paged attention requires GPU tensors")
+    if q.dtype != torch.bfloat16 or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("paged attention requires BF16 Q/K/V")
+    if q.shape[-1] != _HEAD_DIM or q.shape[2] % _PAGE_SIZE:
+        raise ValueError("paged attention requires head_dim=128 and N divisible by 4")
+
+
 @torch.no_grad()
 def paged_attention(
     q: torch.Tensor,
@@ -38,16 +52,7 @@ def paged_attention(
     return_lse: bool = False,
 ):
     """Weighted sparse attention over the plan's KV4 blocks; returns o (and base-2 lse)."""
-    if q.ndim != 4 or q.shape != k.shape or q.shape != v.shape:
-        raise ValueError("Q/K/V must have the same [B,H,N,D] shape")
-    if q.device != k.device or q.device != v.device:
-        raise ValueError("Q/K/V must be on the same CUDA device")
-    if q.device.type != "cuda":
-        raise ValueError("paged attention requires GPU tensors")
-    if q.dtype != torch.bfloat16 or k.dtype != q.dtype or v.dtype != q.dtype:
-        raise ValueError("paged attention requires BF16 Q/K/V")
-    if q.shape[-1] != _HEAD_DIM or q.shape[2] % _PAGE_SIZE:
-        raise ValueError("paged attention requires head_dim=128 and N divisible by 4")
+    check_prefill_inputs(q, k, v)
     batch, heads, tokens, dim = q.shape
     batch_heads = batch * heads
     rows = batch_heads * math.ceil(tokens / _QUERY_BLOCK)
@@ -94,4 +99,35 @@ def _prefill_kv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ids: torch.Te
         _lib.check(lib.ab_paged_prefill_kv(
             _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), batch * heads, tokens, k.shape[2], _lib.ptr(ids),
             _lib.ptr(weights), ids.shape[1], _lib.ptr(output), _lib.ptr(lse), _lib.stream(q.device)))
+    return (output, lse) if return_lse else output
+
+
+def _remap_ids(ids: torch.Tensor, page_map: torch.Tensor) -> torch.Tensor:
+    """int32 ids -> page_map[ids] (ab_remap_ids; ids clamped into the map)."""
+    ids = ids.to(torch.int32).contiguous()
+    out = torch.empty_like(ids)
+    lib = _lib.load()
+    with torch.cuda.device(ids.device):
+        _lib.check(lib.ab_remap_ids(_lib.ptr(ids), ids.numel(), _lib.ptr(page_map), page_map.numel(),
+                                    _lib.ptr(out), _lib.stream(ids.device)))
+    return out
+
+
+def _prefill_ordered(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, order: torch.Tensor, ids: torch.Tensor,
+                     weights: torch.Tensor, *, return_lse: bool = False):
+    """The weighted prefill of the token-permuted q (query t is stored row
+    order[t]) over stored-order k/v pages (ab_paged_prefill_ordered); output
+    and lse in stored order. Shapes are checked by the callers."""
+    batch, heads, tokens, _ = q.shape
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    ids = ids.to(torch.int32).contiguous()
+    weights = weights.to(torch.float32).contiguous()
+    output = torch.empty_like(q)
+    lse = torch.empty((batch, heads, tokens), dtype=torch.float32, device=q.device) if return_lse else None
+    lib = _lib.load()
+    with torch.cuda.device(q.device):
+        _lib.check(lib.ab_paged_prefill_ordered(
+            _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(order), batch * heads, tokens, _lib.ptr(ids),
+            _lib.ptr(weights), ids.shape[1], _lib.ptr(output),
+            _lib.ptr(lse), _lib.stream(q.device)))
     return (output, lse) if return_lse else output

@@ -26,7 +26,7 @@ import torch
 
 from . import _lib
 from .attention import SamplePlan, apply_plan, build_plan
-from .paged import _prefill_kv
+from .paged import _prefill_kv, _prefill_ordered, _remap_ids
 
 _QUERY_BLOCK = 128
 _PAGE = 4
@@ -56,6 +56,81 @@ def cube_order(grid):
     inner = ((tt % 4) * 4 + hh % 4) * 4 + ww % 4
     order = torch.argsort((cube * 64 + inner).reshape(-1))
     return order, torch.argsort(order)
+
+
+_CUBE_MAPS = {}
+
+
+def _cube_maps(grid, device):
+    """(order, page_map) of a latent grid (T, H, W) on ``device``, cached:
+    order int32 [T*H*W] (cube position t is stored token order[t]) and
+    page_map int32 [T*H*W/4] (cube-order KV4 block j is stored block
+    page_map[j]). Every cube-order KV4 block must be 4 consecutive stored
+    tokens starting at a multiple of 4, which holds when W % 4 == 0."""
+    key = (tuple(int(s) for s in grid), str(device))
+    if key not in _CUBE_MAPS:
+        order, _ = cube_order(grid)
+        if order.numel() % _PAGE:
+            raise ValueError("the cube layout needs T*H*W divisible by 4")
+        quads = order.reshape(-1, _PAGE)
+        if not bool(torch.all(quads == quads[:, :1] + torch.arange(_PAGE))) or not bool(torch.all(quads[:, 0] % _PAGE == 0)):
+            raise ValueError("the cube layout's KV4 blocks must be 4 consecutive stored tokens (latent width % 4 == 0)")
+        _CUBE_MAPS[key] = (order.to(torch.int32).to(device), (quads[:, 0] // _PAGE).to(torch.int32).to(device))
+    return _CUBE_MAPS[key]
+
+
+def _check_cube(q: torch.Tensor, grid):
+    t, h, w = (int(s) for s in grid)
+    if q.ndim != 4 or q.shape[2] != t * h * w:
+        raise ValueError("the cube layout needs [B,H,N,128] tensors with N = T*H*W of the latent grid")
+
+
+@torch.no_grad()
+def cube_plan(q: torch.Tensor, k: torch.Tensor, grid, *, sample_pages: int = 64, seed: int = 42) -> SamplePlan:
+    """build_plan in the cube token layout (reference: use_cube_layout,
+    video.py:90-126, which runs attention on cube-ordered tensors) for q, k
+    kept in their stored (raster) order: equal to build_plan(q[:, :, order],
+    k[:, :, order], ...) with ``order`` from cube_order(grid), without
+    permuting q or k. The plan's ids are cube-order KV4 blocks."""
+    from . import _C
+    from .attention import _build_plan
+
+    _check_cube(q, grid)
+    order, _ = _cube_maps(grid, q.device)
+    return _build_plan(q, k, sample_pages, seed, lambda qc, kc: _C.ibcs_ordered(qc, kc, order))
+
+
+@torch.no_grad()
+def apply_cube_plan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan: SamplePlan, grid, *,
+                    return_lse: bool = False):
+    """apply_plan in the cube token layout on stored-order q, k, v: equal to
+    apply_plan on the cube-ordered tensors with the output (and lse) scattered
+    back to stored order. K/V pages are read in place (cube-order ids are
+    remapped to stored pages) and queries are gathered and scattered by the
+    prefill, so nothing is permuted in memory."""
+    from .paged import check_prefill_inputs
+
+    check_prefill_inputs(q, k, v)
+    _check_cube(q, grid)
+    batch, heads, tokens, _ = q.shape
+    rows = batch * heads * math.ceil(tokens / _QUERY_BLOCK)
+    descriptor, log_weights = plan
+    if descriptor.ndim != 3 or descriptor.shape != log_weights.shape or descriptor.shape[0] != rows \
+            or descriptor.shape[-1] != 32:
+        raise ValueError(f"descriptor and log_weights must share [{rows}, pages, 32] shape")
+    order, page_map = _cube_maps(grid, q.device)
+    ids = _remap_ids(descriptor.reshape(rows, -1), page_map)
+    return _prefill_ordered(q, k, v, order, ids, log_weights.reshape(rows, -1), return_lse=return_lse)
+
+
+@torch.no_grad()
+def cube_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, grid, *, sample_pages: int = 64,
+                   seed: int = 42) -> torch.Tensor:
+    """ab_attention in the cube token layout on stored-order tensors; the
+    output is in stored order (the reference gathers the hidden states into
+    cube order once and scatters them back after the last block,
+    video.py:90-126)."""
+    return apply_cube_plan(q, k, v, cube_plan(q, k, grid, sample_pages=sample_pages, seed=seed), grid)
 
 
 def _check_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):

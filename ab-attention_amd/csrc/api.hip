@@ -15,7 +15,7 @@ namespace ab {
 
 int64_t lse_stride(int64_t fb);
 int launch_cluster_pool(const void* q, const void* k, int64_t bh, int64_t n, void* centroids, float* pops,
-                        void* pooled, float qk_scale_log2, hipStream_t stream);
+                        void* pooled, float qk_scale_log2, const int32_t* order, hipStream_t stream);
 int launch_lse(const void* centroids, const void* pooled, int64_t bh, int64_t n, void* lse, float* lse_max,
                float* lse_den, hipStream_t stream);
 int launch_masses(const void* lse, const float* pops, const float* lse_max, const float* lse_den, int64_t rows,
@@ -25,7 +25,9 @@ int launch_sip(const float* scores, const float* offsets, int64_t rows, int64_t 
 bool sip_fits(int64_t population);
 int launch_prefill(const void* q, const void* k, const void* v, int64_t bh, int64_t n, int64_t n_kv,
                    const int32_t* ids, const float* logw, int64_t samples, void* out, float* lse,
-                   hipStream_t stream);
+                   const int32_t* order, hipStream_t stream);
+int launch_remap_ids(const int32_t* ids, int64_t count, const int32_t* map, int64_t map_len, int32_t* out,
+                     hipStream_t stream);
 int launch_merge(const void* oa, const float* sa, const void* ob, const float* sb, int64_t count, void* out,
                  float* s_out, hipStream_t stream);
 
@@ -118,7 +120,7 @@ int ab_ibcs_cluster_pool(const void* q, const void* k, int64_t batch_heads, int6
     if (!aligned16(q) || !aligned16(k) || !aligned16(pooled_keys))
         return set_error(AB_ERR_INVALID, "ibcs: q, k and pooled keys must be 16-byte aligned");
     return launch_cluster_pool(q, k, batch_heads, tokens, centroids, populations, pooled_keys, qk_scale_log2(),
-                               static_cast<hipStream_t>(stream));
+                               nullptr, static_cast<hipStream_t>(stream));
 }
 
 int ab_ibcs_lse(const void* centroids, const void* pooled_keys, int64_t batch_heads, int64_t tokens,
@@ -144,10 +146,16 @@ int ab_ibcs_masses(const void* block_lse, const float* populations, const float*
                          static_cast<hipStream_t>(stream));
 }
 
-int ab_ibcs(const void* q, const void* k, int64_t batch_heads, int64_t tokens, void* workspace,
-            size_t workspace_bytes, float* scores, void* stream) {
+}  // extern "C"
+
+namespace {
+// The whole IBCS chain, with the query/key tokens read through `order`
+// (nullptr: the stored order).
+int ibcs_chain(const void* q, const void* k, const int32_t* order, int64_t batch_heads, int64_t tokens,
+               void* workspace, size_t workspace_bytes, float* scores, void* stream) {
     if (int rc = check_qk_shape("ibcs", batch_heads, tokens)) return rc;
     if (!q || !k || !workspace || !scores) return set_error(AB_ERR_INVALID, "ibcs: null pointer");
+    if (!aligned16(q) || !aligned16(k)) return set_error(AB_ERR_INVALID, "ibcs: q and k must be 16-byte aligned");
     const IbcsLayout L = ibcs_layout(batch_heads, tokens);
     if (workspace_bytes < L.total)
         return set_error(AB_ERR_INVALID, "ibcs: workspace of %zu bytes is smaller than the %zu required",
@@ -155,8 +163,9 @@ int ab_ibcs(const void* q, const void* k, int64_t batch_heads, int64_t tokens, v
     if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
         return set_error(AB_ERR_INVALID, "ibcs: workspace must be 256-byte aligned");
     char* ws = static_cast<char*>(workspace);
-    if (int rc = ab_ibcs_cluster_pool(q, k, batch_heads, tokens, ws + L.centroids,
-                                      reinterpret_cast<float*>(ws + L.pops), ws + L.pooled, stream))
+    if (int rc = launch_cluster_pool(q, k, batch_heads, tokens, ws + L.centroids,
+                                     reinterpret_cast<float*>(ws + L.pops), ws + L.pooled, qk_scale_log2(), order,
+                                     static_cast<hipStream_t>(stream)))
         return rc;
     if (int rc = ab_ibcs_lse(ws + L.centroids, ws + L.pooled, batch_heads, tokens, ws + L.lse,
                              reinterpret_cast<float*>(ws + L.lse_max), reinterpret_cast<float*>(ws + L.lse_den),
@@ -165,6 +174,20 @@ int ab_ibcs(const void* q, const void* k, int64_t batch_heads, int64_t tokens, v
     return ab_ibcs_masses(ws + L.lse, reinterpret_cast<const float*>(ws + L.pops),
                           reinterpret_cast<const float*>(ws + L.lse_max),
                           reinterpret_cast<const float*>(ws + L.lse_den), L.rows, L.fb, scores, stream);
+}
+}  // namespace
+
+extern "C" {
+
+int ab_ibcs(const void* q, const void* k, int64_t batch_heads, int64_t tokens, void* workspace,
+            size_t workspace_bytes, float* scores, void* stream) {
+    return ibcs_chain(q, k, nullptr, batch_heads, tokens, workspace, workspace_bytes, scores, stream);
+}
+
+int ab_ibcs_ordered(const void* q, const void* k, const int32_t* order, int64_t batch_heads, int64_t tokens,
+                    void* workspace, size_t workspace_bytes, float* scores, void* stream) {
+    if (!order) return set_error(AB_ERR_INVALID, "ibcs: null token order");
+    return ibcs_chain(q, k, order, batch_heads, tokens, workspace, workspace_bytes, scores, stream);
 }
 
 int ab_sip(const float* scores, const float* offsets, int64_t rows, int64_t population, int64_t samples,
@@ -212,8 +235,36 @@ int ab_paged_prefill_kv(const void* q, const void* k, const void* v, int64_t bat
         return set_error(AB_ERR_INVALID, "paged_prefill: ids and log_weights must be 16-byte aligned");
     const int64_t rows = batch_heads * qb;
     if (rows * samples > (int64_t(1) << 40)) return set_error(AB_ERR_INVALID, "paged_prefill: plan too large");
-    return launch_prefill(q, k, v, batch_heads, q_tokens, kv_tokens, ids, log_weights, samples, out, lse,
+    return launch_prefill(q, k, v, batch_heads, q_tokens, kv_tokens, ids, log_weights, samples, out, lse, nullptr,
                           static_cast<hipStream_t>(stream));
+}
+
+int ab_paged_prefill_ordered(const void* q, const void* k, const void* v, const int32_t* order,
+                             int64_t batch_heads, int64_t tokens, const int32_t* ids, const float* log_weights,
+                             int64_t samples, void* out, float* lse, void* stream) {
+    if (!order) return set_error(AB_ERR_INVALID, "paged_prefill: null token order");
+    if (int rc = check_qk_shape("paged_prefill", batch_heads, tokens)) return rc;
+    if (samples <= 0 || samples % kBlocksPerPage)
+        return set_error(AB_ERR_INVALID, "paged_prefill: samples must be a positive multiple of 32");
+    if (!q || !k || !v || !ids || !log_weights || !out)
+        return set_error(AB_ERR_INVALID, "paged_prefill: null pointer");
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || (reinterpret_cast<uintptr_t>(out) & 7u))
+        return set_error(AB_ERR_INVALID, "paged_prefill: q/k/v must be 16-byte and out 8-byte aligned");
+    if (!aligned16(ids) || !aligned16(log_weights))
+        return set_error(AB_ERR_INVALID, "paged_prefill: ids and log_weights must be 16-byte aligned");
+    const int64_t qb = (tokens + kQueryBlock - 1) / kQueryBlock;
+    if (batch_heads > 65535 || qb > 65535) return set_error(AB_ERR_INVALID, "paged_prefill: grid too large");
+    return launch_prefill(q, k, v, batch_heads, tokens, tokens, ids, log_weights, samples, out, lse, order,
+                          static_cast<hipStream_t>(stream));
+}
+
+int ab_remap_ids(const int32_t* ids, int64_t count, const int32_t* map, int64_t map_len, int32_t* out,
+                 void* stream) {
+    if (count < 0 || map_len <= 0 || map_len > kMaxKvBlocks)
+        return set_error(AB_ERR_INVALID, "remap_ids: bad count or map length");
+    if (count > 0 && (!ids || !map || !out)) return set_error(AB_ERR_INVALID, "remap_ids: null pointer");
+    if (count > (int64_t(1) << 40)) return set_error(AB_ERR_INVALID, "remap_ids: too many ids");
+    return launch_remap_ids(ids, count, map, map_len, out, static_cast<hipStream_t>(stream));
 }
 
 int ab_merge_states(const void* o_a, const float* lse_a, const void* o_b, const float* lse_b, int64_t count,

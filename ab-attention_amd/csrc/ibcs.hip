@@ -89,7 +89,7 @@ __device__ __forceinline__ float block_elem(const uint32_t* block, int row, int 
 __global__ __launch_bounds__(kClusterThreads) void cluster_pool_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     uint16_t* __restrict__ centroids, float* __restrict__ pops, uint16_t* __restrict__ pooled,
-    int64_t n, int64_t qb, float qk_scale_log2) {
+    int64_t n, int64_t qb, float qk_scale_log2, const int32_t* __restrict__ order) {
     __shared__ uint32_t block[kQueryBlock * kRowWords];
     __shared__ float center_row[kHeadDim];
     __shared__ float s_val[2];
@@ -102,12 +102,17 @@ __global__ __launch_bounds__(kClusterThreads) void cluster_pool_kernel(
     const int valid = static_cast<int>(min<int64_t>(kQueryBlock, n - base));
     const int64_t row = bh * qb + blk;
 
+    // Token t of the head is row src_row(t) of Q and K: t itself, or order[t]
+    // for a permuted token layout (clamped into the head).
+    auto src_row = [&](int64_t t) -> int64_t {
+        return order ? min<int64_t>(max(order[t], 0), n - 1) : t;
+    };
     // Stage the query block (zero rows past the sequence end).
-    const u32x4* src = reinterpret_cast<const u32x4*>(q + (bh * n + base) * kHeadDim);
+    const u32x4* qhead = reinterpret_cast<const u32x4*>(q + bh * n * kHeadDim);
     for (int idx = tid; idx < kQueryBlock * 16; idx += kClusterThreads) {
         const int r = idx >> 4, c = idx & 15;
         u32x4 v = {0u, 0u, 0u, 0u};
-        if (r < valid) v = src[idx];
+        if (r < valid) v = qhead[src_row(base + r) * 16 + c];
         uint32_t* dst = block + r * kRowWords + c * 4;
         dst[0] = v.x;
         dst[1] = v.y;
@@ -209,13 +214,13 @@ __global__ __launch_bounds__(kClusterThreads) void cluster_pool_kernel(
     }
 
     // Pool the same tokens' keys: bf16(0.5 * (k_2r + k_2r+1)) (:244-266).
-    const u32x4* ksrc = reinterpret_cast<const u32x4*>(k + (bh * n + base) * kHeadDim);
+    const u32x4* khead = reinterpret_cast<const u32x4*>(k + bh * n * kHeadDim);
     u32x4* kdst = reinterpret_cast<u32x4*>(pooled + (bh * (n / 2) + base / 2) * kHeadDim);
     const int pairs = valid / 2;
     for (int idx = tid; idx < pairs * 16; idx += kClusterThreads) {
         const int p = idx >> 4, c = idx & 15;
-        const u32x4 a = ksrc[(2 * p) * 16 + c];
-        const u32x4 b = ksrc[(2 * p + 1) * 16 + c];
+        const u32x4 a = khead[src_row(base + 2 * p) * 16 + c];
+        const u32x4 b = khead[src_row(base + 2 * p + 1) * 16 + c];
         u32x4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -290,13 +295,13 @@ __global__ __launch_bounds__(kMassThreads) void masses_kernel(
 int64_t lse_stride(int64_t fb) { return (fb + 63) / 64 * 64; }
 
 int launch_cluster_pool(const void* q, const void* k, int64_t bh, int64_t n, void* centroids,
-                        float* pops, void* pooled, float qk_scale_log2, hipStream_t stream) {
+                        float* pops, void* pooled, float qk_scale_log2, const int32_t* order, hipStream_t stream) {
     const int64_t qb = (n + kQueryBlock - 1) / kQueryBlock;
     dim3 grid(static_cast<unsigned>(qb), static_cast<unsigned>(bh));
     hipLaunchKernelGGL(cluster_pool_kernel, grid, dim3(kClusterThreads), 0, stream,
                        static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                        static_cast<uint16_t*>(centroids), pops, static_cast<uint16_t*>(pooled), n, qb,
-                       qk_scale_log2);
+                       qk_scale_log2, order);
     return check_launch("cluster_pool_kernel");
 }
 

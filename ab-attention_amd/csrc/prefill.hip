@@ -97,7 +97,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const int32_t* __restrict__ ids, const float* __restrict__ logw, uint16_t* __restrict__ out,
     float* __restrict__ lse, int64_t n, int64_t n_kv, int64_t qb, int64_t rows, int fb, int samples,
-    float scale_log2) {
+    float scale_log2, const int32_t* __restrict__ order) {
     extern __shared__ __align__(16) unsigned char smem[];
 
     // XCD-aware row order. The hardware deals workgroups round-robin over the
@@ -118,12 +118,15 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
     const int qi = lane & 31, half = lane >> 5;
     const int64_t token = blk * kQueryBlock + wave * 32 + qi;
     const bool valid_q = token < n;
+    // Row of Q / out / lse holding this token: the token itself, or
+    // order[token] for a permuted token layout (clamped into the head).
+    const int64_t qrow_index = !valid_q ? 0 : order ? min<int64_t>(max(order[token], 0), n - 1) : token;
     const int tiles = samples / kTilePages;
 
     // Q as the B operand of S^T = K Q^T: dims 16s + 8*half .. +8.
     bf16x8 bq[8];
     {
-        const uint16_t* qrow = q + (bh * n + (valid_q ? token : 0)) * kHeadDim + 8 * half;
+        const uint16_t* qrow = q + (bh * n + qrow_index) * kHeadDim + 8 * half;
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
             u32x4 val = {0u, 0u, 0u, 0u};
@@ -384,7 +387,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
     const float l_tot = __uint_as_float(lsw[0]) + __uint_as_float(lsw[1]);
     if (valid_q) {
         const float inv = 1.0f / l_tot;
-        uint16_t* orow = out + (bh * n + token) * kHeadDim;
+        uint16_t* orow = out + (bh * n + qrow_index) * kHeadDim;
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -393,7 +396,20 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
                                   pack_bf16(o_acc[dt][4 * g + 2] * inv, o_acc[dt][4 * g + 3] * inv)};
                 *reinterpret_cast<u32x2*>(orow + 32 * dt + 8 * g + 4 * half) = pk;
             }
-        if (lse != nullptr && half == 0) lse[bh * n + token] = m_run + log2f(l_tot);
+        if (lse != nullptr && half == 0) lse[bh * n + qrow_index] = m_run + log2f(l_tot);
+    }
+}
+
+// Plan ids of a permuted token layout -> KV4 pages of the stored layout:
+// out[i] = map[clamp(ids[i])], 4 ids per thread.
+__global__ __launch_bounds__(256) void remap_ids_kernel(const int32_t* __restrict__ ids, int64_t count,
+                                                        const int32_t* __restrict__ map, int map_len,
+                                                        int32_t* __restrict__ out) {
+    const int64_t i0 = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int64_t i = i0 + e;
+        if (i < count) out[i] = map[min(max(ids[i], 0), map_len - 1)];
     }
 }
 
@@ -437,9 +453,18 @@ int launch_merge(const void* oa, const float* sa, const void* ob, const float* s
     return check_launch("merge_kernel");
 }
 
+int launch_remap_ids(const int32_t* ids, int64_t count, const int32_t* map, int64_t map_len, int32_t* out,
+                     hipStream_t stream) {
+    if (count == 0) return 0;
+    const int64_t threads = (count + 3) / 4;
+    hipLaunchKernelGGL(remap_ids_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, stream, ids,
+                       count, map, static_cast<int>(map_len), out);
+    return check_launch("remap_ids_kernel");
+}
+
 int launch_prefill(const void* q, const void* k, const void* v, int64_t bh, int64_t n, int64_t n_kv,
                    const int32_t* ids, const float* logw, int64_t samples, void* out, float* lse,
-                   hipStream_t stream) {
+                   const int32_t* order, hipStream_t stream) {
     const int64_t qb = (n + kQueryBlock - 1) / kQueryBlock;
     const int64_t rows = bh * qb;
     if (samples % kTilePages != 0)
@@ -460,7 +485,7 @@ int launch_prefill(const void* q, const void* k, const void* v, int64_t bh, int6
     hipLaunchKernelGGL(prefill_kernel, dim3(static_cast<unsigned>(per_xcd * 8 * bh)), dim3(kPfThreads), kLdsBytes,
                        stream, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                        static_cast<const uint16_t*>(v), ids, logw, static_cast<uint16_t*>(out), lse, n, n_kv, qb, rows,
-                       static_cast<int>(n_kv / kKvBlock), static_cast<int>(samples), scale_log2);
+                       static_cast<int>(n_kv / kKvBlock), static_cast<int>(samples), scale_log2, order);
     return check_launch("prefill_kernel");
 }
 

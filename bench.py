@@ -141,6 +141,14 @@ def main() -> int:
     samples = cfg.sample_pages * 32
     rows, fb, f_pre, b_sel = work_figures(bh, n, samples)
 
+    if cfg.cube_layout:
+        # c4: the cube token layout computed in place on raster-order tensors
+        # (same results as permuting Q/K/V, attending and permuting back).
+        from ab_attention.video import apply_cube_plan, cube_plan
+
+        build_plan = lambda q_, k_, **kw: cube_plan(q_, k_, cfg.grid, **kw)  # noqa: E731
+        apply_plan = lambda q_, k_, v_, plan_: apply_cube_plan(q_, k_, v_, plan_, cfg.grid)  # noqa: E731
+
     def step():
         plan = build_plan(q, k, sample_pages=cfg.sample_pages, seed=42)
         return apply_plan(q, k, v, plan)

@@ -105,6 +105,31 @@ int ab_paged_prefill_kv(const void *q, const void *k, const void *v, int64_t bat
 int ab_merge_states(const void *o_a, const float *lse_a, const void *o_b, const float *lse_b, int64_t count,
                     void *out, float *lse_out, void *stream);
 
+/* ---- Permuted token layouts (cube layout) ----------------------------------
+ * The reference's use_cube_layout (ab_attention/video.py:90-126) gathers the
+ * hidden states into 4x4x4-cube order before the first block and scatters
+ * them back after the last, so attention sees tensors in cube order. These
+ * entry points compute the same attention on tensors kept in their stored
+ * order: order int32 [tokens] gives, for cube position t, the stored token
+ * order[t] (a permutation; the same for every head).
+ * ab_ibcs_ordered: ab_ibcs of the permuted q, k (scores over cube-order KV4
+ *   blocks), reading tokens through `order`.
+ * ab_remap_ids: out[i] = map[ids[i]] (ids clamped into [0, map_len)); with
+ *   map[j] = order[4j] / 4 it turns cube-order KV4 ids into stored-order ones,
+ *   which is valid when every cube-order KV4 block is 4 consecutive stored
+ *   tokens starting at a multiple of 4 (true for the cube layout when the
+ *   latent width is a multiple of 4).
+ * ab_paged_prefill_ordered: ab_paged_prefill of the permuted q with stored
+ *   k, v, ids already remapped to stored-order KV4 pages; query t is read from
+ *   and written to stored row order[t] (out and lse in stored order). */
+int ab_ibcs_ordered(const void *q, const void *k, const int32_t *order, int64_t batch_heads, int64_t tokens,
+                    void *workspace, size_t workspace_bytes, float *scores, void *stream);
+int ab_remap_ids(const int32_t *ids, int64_t count, const int32_t *map, int64_t map_len, int32_t *out,
+                 void *stream);
+int ab_paged_prefill_ordered(const void *q, const void *k, const void *v, const int32_t *order,
+                             int64_t batch_heads, int64_t tokens, const int32_t *ids, const float *log_weights,
+                             int64_t samples, void *out, float *lse, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

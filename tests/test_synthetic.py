@@ -1,6 +1,8 @@
 """Seeded input generator and the cube-layout permutation (CPU)."""
 import itertools
 
+import pytest
+
 import torch
 
 from ab_attention.synthetic import CONFIGS, make_qkv
@@ -53,3 +55,17 @@ def test_cube_order_matches_bruteforce():
 def test_cube_layout_order_pixel_shape():
     order, _ = cube_layout_order(num_frames=81, height=720, width=1280)
     assert len(order) == 21 * 45 * 80
+
+
+def test_cube_page_map():
+    """Every cube-order KV4 block is 4 consecutive raster tokens when W % 4 == 0;
+    the page map sends cube block j to raster block order[4j] / 4."""
+    from ab_attention.video import _cube_maps
+
+    for grid in [(21, 45, 80), (6, 10, 12), (5, 7, 4)]:
+        order, page_map = _cube_maps(grid, "cpu")
+        quads = order.reshape(-1, 4).long()
+        assert torch.equal(quads, 4 * page_map.long()[:, None] + torch.arange(4))
+        assert torch.equal(torch.sort(order.long()).values, torch.arange(order.numel()))
+    with pytest.raises(ValueError):
+        _cube_maps((4, 6, 6), "cpu")
