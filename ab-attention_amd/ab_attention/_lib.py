@@ -37,9 +37,11 @@ SIGNATURES = {
     "ab_ibcs_ordered": (ctypes.c_int, [_P, _P, _P, _I64, _I64, _P, _SZ, _P, _P]),
     "ab_remap_ids": (ctypes.c_int, [_P, _I64, _P, _I64, _P, _P]),
     "ab_paged_prefill_ordered": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _P, _P, _I64, _P, _P, _P]),
+    "ab_kv4_transpose": (ctypes.c_int, [_P, _I64, _I64, _P, _P]),
+    "ab_paged_prefill_kv4t": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _P, _P, _P]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 _lib = None
 
 

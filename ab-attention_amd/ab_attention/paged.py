@@ -2,10 +2,13 @@
 
 ``paged_attention`` keeps the reference's signature, validation (ValueError)
 and output/LSE layout (ab_attention/flashinfer_backend.py:164-242). The
-arithmetic is ``ab_paged_prefill`` in libab_attention_hip.so: a bf16 MFMA
-flash-attention kernel that reads each row's KV4 blocks straight from K/V by
-their per-head ids and adds the SIP weight of each block to its logits
+arithmetic is ``ab_paged_prefill_kv`` in libab_attention_hip.so: a bf16 MFMA
+flash-attention kernel that reads each row's KV4 blocks straight from K and
+V by their per-head ids and adds the SIP weight of each block to its logits
 (the reference's ABSipAttention variant, flashinfer_backend.py:30-59).
+``kv4_transpose`` produces the library's alternative V layout (each 4-key
+page stored dim-major, for ``ab_paged_prefill_kv4t``); it is not used here:
+on gfx950 it saves the prefill under 1 % and the transpose pass costs more.
 
 The reference translates per-head ids into a global page table and caches it
 per descriptor (flashinfer_backend.py:62-74, :202-217); the kernel here
@@ -25,6 +28,44 @@ from . import _lib
 _HEAD_DIM = 128
 _QUERY_BLOCK = 128
 _PAGE_SIZE = 4
+
+
+def kv4_transpose(v: torch.Tensor) -> torch.Tensor:
+    """V bf16 [B,H,Nk,128] (Nk % 4 == 0) -> the prefill's KV4-transposed layout
+    [B,H,Nk/4,128,4] (ab_kv4_transpose): each 4-key page stored dim-major, so
+    the kernel's PV operand reads are plain 8-byte LDS reads."""
+    v = v.contiguous()
+    batch, heads, tokens, dim = v.shape
+    out = torch.empty((batch, heads, tokens // _PAGE_SIZE, dim, _PAGE_SIZE), dtype=v.dtype, device=v.device)
+    lib = _lib.load()
+    with torch.cuda.device(v.device):
+        _lib.check(lib.ab_kv4_transpose(_lib.ptr(v), batch * heads, tokens, _lib.ptr(out), _lib.stream(v.device)))
+    return out
+
+
+def _prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
+             order: torch.Tensor | None, return_lse: bool):
+    """The weighted prefill of row-major q, k, v: ab_paged_prefill_kv, or
+    ab_paged_prefill_ordered when a query token order is given; ids/weights
+    [rows, S]. Shapes are checked by the callers."""
+    batch, heads, tokens, _ = q.shape
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    ids = ids.to(torch.int32).contiguous()
+    weights = weights.to(torch.float32).contiguous()
+    output = torch.empty_like(q)
+    lse = torch.empty((batch, heads, tokens), dtype=torch.float32, device=q.device) if return_lse else None
+    lib = _lib.load()
+    with torch.cuda.device(q.device):
+        if order is None:
+            rc = lib.ab_paged_prefill_kv(
+                _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), batch * heads, tokens, k.shape[2], _lib.ptr(ids),
+                _lib.ptr(weights), ids.shape[-1], _lib.ptr(output), _lib.ptr(lse), _lib.stream(q.device))
+        else:
+            rc = lib.ab_paged_prefill_ordered(
+                _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(order), batch * heads, tokens, _lib.ptr(ids),
+                _lib.ptr(weights), ids.shape[-1], _lib.ptr(output), _lib.ptr(lse), _lib.stream(q.device))
+        _lib.check(rc)
+    return (output, lse) if return_lse else output
 
 
 def check_prefill_inputs(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
@@ -63,43 +104,19 @@ def paged_attention(
         raise ValueError("descriptor and log_weights must be on the Q device")
 
     samples = descriptor.shape[1] * 32
-    q = q.contiguous()
-    k = k.contiguous()
-    v = v.contiguous()
-    ids = descriptor.to(torch.int32).contiguous()
-    weights = log_weights.to(torch.float32).contiguous()
-    output = torch.empty_like(q)
-    lse = torch.empty((batch, heads, tokens), dtype=torch.float32, device=q.device) if return_lse else None
-    lib = _lib.load()
-    with torch.cuda.device(q.device):
-        _lib.check(lib.ab_paged_prefill(
-            _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), batch_heads, tokens, _lib.ptr(ids),
-            _lib.ptr(weights), samples, _lib.ptr(output), _lib.ptr(lse), _lib.stream(q.device)))
-    if not return_lse:
-        return output
-    return output, lse
+    return _prefill(q, k, v, descriptor.reshape(rows, samples), log_weights.reshape(rows, samples), None,
+                    return_lse)
 
 
 def _prefill_kv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
                 *, return_lse: bool = False):
-    """The weighted prefill with K/V of their own length (ab_paged_prefill_kv).
+    """The weighted prefill with K/V of their own length.
 
     q bf16 [B,H,Nq,128], k/v bf16 [B,H,Nk,128] with Nk % 4 == 0, ids int32 /
     weights f32 [B*H*ceil(Nq/128), S] with S % 8 == 0 (per-head KV4 ids; a -inf
     weight removes its block). Shapes are checked by the callers.
     """
-    batch, heads, tokens, _ = q.shape
-    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
-    ids = ids.to(torch.int32).contiguous()
-    weights = weights.to(torch.float32).contiguous()
-    output = torch.empty_like(q)
-    lse = torch.empty((batch, heads, tokens), dtype=torch.float32, device=q.device) if return_lse else None
-    lib = _lib.load()
-    with torch.cuda.device(q.device):
-        _lib.check(lib.ab_paged_prefill_kv(
-            _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), batch * heads, tokens, k.shape[2], _lib.ptr(ids),
-            _lib.ptr(weights), ids.shape[1], _lib.ptr(output), _lib.ptr(lse), _lib.stream(q.device)))
-    return (output, lse) if return_lse else output
+    return _prefill(q, k, v, ids, weights, None, return_lse)
 
 
 def _remap_ids(ids: torch.Tensor, page_map: torch.Tensor) -> torch.Tensor:
@@ -116,18 +133,6 @@ def _remap_ids(ids: torch.Tensor, page_map: torch.Tensor) -> torch.Tensor:
 def _prefill_ordered(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, order: torch.Tensor, ids: torch.Tensor,
                      weights: torch.Tensor, *, return_lse: bool = False):
     """The weighted prefill of the token-permuted q (query t is stored row
-    order[t]) over stored-order k/v pages (ab_paged_prefill_ordered); output
-    and lse in stored order. Shapes are checked by the callers."""
-    batch, heads, tokens, _ = q.shape
-    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
-    ids = ids.to(torch.int32).contiguous()
-    weights = weights.to(torch.float32).contiguous()
-    output = torch.empty_like(q)
-    lse = torch.empty((batch, heads, tokens), dtype=torch.float32, device=q.device) if return_lse else None
-    lib = _lib.load()
-    with torch.cuda.device(q.device):
-        _lib.check(lib.ab_paged_prefill_ordered(
-            _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(order), batch * heads, tokens, _lib.ptr(ids),
-            _lib.ptr(weights), ids.shape[1], _lib.ptr(output),
-            _lib.ptr(lse), _lib.stream(q.device)))
-    return (output, lse) if return_lse else output
+    order[t]) over stored-order k/v pages; output and lse in stored order.
+    Shapes are checked by the callers."""
+    return _prefill(q, k, v, ids, weights, order.to(torch.int32).contiguous(), return_lse)

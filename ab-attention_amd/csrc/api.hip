@@ -23,9 +23,10 @@ int launch_masses(const void* lse, const float* pops, const float* lse_max, cons
 int launch_sip(const float* scores, const float* offsets, int64_t rows, int64_t population, int64_t samples,
                int32_t* ids, float* logw, hipStream_t stream);
 bool sip_fits(int64_t population);
-int launch_prefill(const void* q, const void* k, const void* v, int64_t bh, int64_t n, int64_t n_kv,
+int launch_prefill(const void* q, const void* k, const void* v, bool v_kv4t, int64_t bh, int64_t n, int64_t n_kv,
                    const int32_t* ids, const float* logw, int64_t samples, void* out, float* lse,
                    const int32_t* order, hipStream_t stream);
+int launch_kv4_transpose(const void* v, int64_t bh, int64_t n_kv, void* vt, hipStream_t stream);
 int launch_remap_ids(const int32_t* ids, int64_t count, const int32_t* map, int64_t map_len, int32_t* out,
                      hipStream_t stream);
 int launch_merge(const void* oa, const float* sa, const void* ob, const float* sb, int64_t count, void* out,
@@ -214,9 +215,11 @@ int ab_paged_prefill(const void* q, const void* k, const void* v, int64_t batch_
     return ab_paged_prefill_kv(q, k, v, batch_heads, tokens, tokens, ids, log_weights, samples, out, lse, stream);
 }
 
-int ab_paged_prefill_kv(const void* q, const void* k, const void* v, int64_t batch_heads, int64_t q_tokens,
-                        int64_t kv_tokens, const int32_t* ids, const float* log_weights, int64_t samples,
-                        void* out, float* lse, void* stream) {
+namespace {
+// Shared validation of the prefill entry points; v_kv4t selects V's layout.
+int paged_prefill_checked(const void* q, const void* k, const void* v, bool v_kv4t, const int32_t* order,
+                          int64_t batch_heads, int64_t q_tokens, int64_t kv_tokens, const int32_t* ids,
+                          const float* log_weights, int64_t samples, void* out, float* lse, void* stream) {
     if (batch_heads <= 0 || q_tokens <= 0 || kv_tokens <= 0)
         return set_error(AB_ERR_INVALID, "paged_prefill: batch_heads and token counts must be positive");
     if (kv_tokens % kKvBlock)
@@ -235,8 +238,16 @@ int ab_paged_prefill_kv(const void* q, const void* k, const void* v, int64_t bat
         return set_error(AB_ERR_INVALID, "paged_prefill: ids and log_weights must be 16-byte aligned");
     const int64_t rows = batch_heads * qb;
     if (rows * samples > (int64_t(1) << 40)) return set_error(AB_ERR_INVALID, "paged_prefill: plan too large");
-    return launch_prefill(q, k, v, batch_heads, q_tokens, kv_tokens, ids, log_weights, samples, out, lse, nullptr,
-                          static_cast<hipStream_t>(stream));
+    return launch_prefill(q, k, v, v_kv4t, batch_heads, q_tokens, kv_tokens, ids, log_weights, samples, out, lse,
+                          order, static_cast<hipStream_t>(stream));
+}
+}  // namespace
+
+int ab_paged_prefill_kv(const void* q, const void* k, const void* v, int64_t batch_heads, int64_t q_tokens,
+                        int64_t kv_tokens, const int32_t* ids, const float* log_weights, int64_t samples,
+                        void* out, float* lse, void* stream) {
+    return paged_prefill_checked(q, k, v, false, nullptr, batch_heads, q_tokens, kv_tokens, ids, log_weights,
+                                 samples, out, lse, stream);
 }
 
 int ab_paged_prefill_ordered(const void* q, const void* k, const void* v, const int32_t* order,
@@ -246,16 +257,27 @@ int ab_paged_prefill_ordered(const void* q, const void* k, const void* v, const 
     if (int rc = check_qk_shape("paged_prefill", batch_heads, tokens)) return rc;
     if (samples <= 0 || samples % kBlocksPerPage)
         return set_error(AB_ERR_INVALID, "paged_prefill: samples must be a positive multiple of 32");
-    if (!q || !k || !v || !ids || !log_weights || !out)
-        return set_error(AB_ERR_INVALID, "paged_prefill: null pointer");
-    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || (reinterpret_cast<uintptr_t>(out) & 7u))
-        return set_error(AB_ERR_INVALID, "paged_prefill: q/k/v must be 16-byte and out 8-byte aligned");
-    if (!aligned16(ids) || !aligned16(log_weights))
-        return set_error(AB_ERR_INVALID, "paged_prefill: ids and log_weights must be 16-byte aligned");
-    const int64_t qb = (tokens + kQueryBlock - 1) / kQueryBlock;
-    if (batch_heads > 65535 || qb > 65535) return set_error(AB_ERR_INVALID, "paged_prefill: grid too large");
-    return launch_prefill(q, k, v, batch_heads, tokens, tokens, ids, log_weights, samples, out, lse, order,
-                          static_cast<hipStream_t>(stream));
+    return paged_prefill_checked(q, k, v, false, order, batch_heads, tokens, tokens, ids, log_weights, samples,
+                                 out, lse, stream);
+}
+
+int ab_kv4_transpose(const void* v, int64_t batch_heads, int64_t kv_tokens, void* v_kv4t, void* stream) {
+    if (batch_heads < 0 || kv_tokens < 0 || kv_tokens % kKvBlock)
+        return set_error(AB_ERR_INVALID, "kv4_transpose: bad shape (kv_tokens must be divisible by 4)");
+    if (batch_heads * kv_tokens == 0) return AB_OK;
+    if (!v || !v_kv4t) return set_error(AB_ERR_INVALID, "kv4_transpose: null pointer");
+    if (!aligned16(v) || !aligned16(v_kv4t))
+        return set_error(AB_ERR_INVALID, "kv4_transpose: buffers must be 16-byte aligned");
+    if (batch_heads * (kv_tokens / kKvBlock) * 16 > (int64_t(0xffffffff) * 256))
+        return set_error(AB_ERR_INVALID, "kv4_transpose: too large");
+    return launch_kv4_transpose(v, batch_heads, kv_tokens, v_kv4t, static_cast<hipStream_t>(stream));
+}
+
+int ab_paged_prefill_kv4t(const void* q, const void* k, const void* v_kv4t, const int32_t* order,
+                          int64_t batch_heads, int64_t q_tokens, int64_t kv_tokens, const int32_t* ids,
+                          const float* log_weights, int64_t samples, void* out, float* lse, void* stream) {
+    return paged_prefill_checked(q, k, v_kv4t, true, order, batch_heads, q_tokens, kv_tokens, ids, log_weights,
+                                 samples, out, lse, stream);
 }
 
 int ab_remap_ids(const int32_t* ids, int64_t count, const int32_t* map, int64_t map_len, int32_t* out,

@@ -93,6 +93,14 @@ __device__ __forceinline__ void wait_and_barrier() {
     asm volatile("s_barrier" ::: "memory");
 }
 
+// kVT selects the layout of V:
+//   false: row-major [n_kv, 128], read with the transposing LDS read (the
+//          tile is swizzled so those reads are conflict free);
+//   true:  KV4-transposed [n_kv/4, 128, 4] (kv4_transpose_kernel): each page
+//          is 128 dims x 4 keys, so the PV operand of a lane (one dim, 8 keys
+//          from two pages) is two plain 8-byte LDS reads, at twice the rate
+//          of the transposing read on gfx950.
+template <bool kVT>
 __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const int32_t* __restrict__ ids, const float* __restrict__ logw, uint16_t* __restrict__ out,
@@ -167,6 +175,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
         k_src[e] = uint32_t(r * 16 + (pos ^ (key & 15))) * 16u;
     }
     const uint32_t v_src = [&] {
+        if (kVT) return uint32_t(lane) * 16u;
         const int m = lane >> 3, sl = (lane >> 1) & 3, h = lane & 1;
         return uint32_t((sl ^ ((m >> 1) & 3)) * 16 + 2 * m + h) * 16u;
     }();
@@ -182,10 +191,10 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
         return c;
     };
     auto dma_k = [&](int u, uint32_t id, int e) {
-        dma16(kbase, id * kPageBytes + k_src[e], lds0 + kKRing + (u % kRing) * kTileBytes + (2 * wave + e) * kPageBytes);
+        dma16(kbase, id * kPageBytes + k_src[e], lds0 + kKRing + (u & (kRing - 1)) * kTileBytes + (2 * wave + e) * kPageBytes);
     };
     auto dma_v = [&](int u, uint32_t id, int e) {
-        dma16(vbase, id * kPageBytes + v_src, lds0 + kVRing + (u % kRing) * kTileBytes + (2 * wave + e) * kPageBytes);
+        dma16(vbase, id * kPageBytes + v_src, lds0 + kVRing + (u & (kRing - 1)) * kTileBytes + (2 * wave + e) * kPageBytes);
     };
     // The four block weights of this lane's keys in tile u: lane register r
     // holds key 8*(r/4) + 4*half + r%4, i.e. page 2(r/4) + half.
@@ -209,15 +218,28 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
         for (int dt = 0; dt < 4; ++dt) v_off[dt] = half * 1024 + (2 * dt + gd) * 128 + 32 * (r ^ dt) + 8 * q4;
     }
     auto read_k = [&](int u, int j) {
-        return *reinterpret_cast<const u32x4*>(smem + kKRing + (u % kRing) * kTileBytes + k_off[j]);
+        return *reinterpret_cast<const u32x4*>(smem + kKRing + (u & (kRing - 1)) * kTileBytes + k_off[j]);
     };
     // PV A operand j of tile u: V^T for k-step j/4, dims 32(j%4) .. +31. MFMA
     // k-index 8*half + 4t + r of k-step ks is key r of tile page 4*ks + 2t +
     // half, on both operands. Lane (group g = lane/16, i = lane%16) does two
     // transposing reads; the source lane 4r + q addresses key r of that page,
     // dims 32dt + 16(g%2) + 4q .. +3, so lane i receives dim 32dt + 16(g%2) + i.
+    // KV4-transposed V: lane (dim 32dt + qi, half) reads that dim's 4 keys of
+    // tile pages 4ks + half (t = 0) and 4ks + 2 + half (t = 1). The two reads
+    // use separate base registers so they stay two ds_read_b64 (a merged
+    // ds_read2st64_b64 is slower).
+    const uint32_t vt0 = kVRing + half * 1024 + qi * 8;
+    uint32_t vt1 = vt0 + 2048;
+    asm volatile("" : "+v"(vt1));
     auto read_v = [&](int u, int j) {
-        const unsigned char* p0 = smem + kVRing + (u % kRing) * kTileBytes + v_off[j & 3] + (j >> 2) * 4096;
+        if (kVT) {
+            const int off = (u & (kRing - 1)) * kTileBytes + (j >> 2) * 4096 + (j & 3) * 256;
+            const u32x2 lo = *reinterpret_cast<const u32x2*>(smem + vt0 + off);
+            const u32x2 hi = *reinterpret_cast<const u32x2*>(smem + vt1 + off);
+            return __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+        }
+        const unsigned char* p0 = smem + kVRing + (u & (kRing - 1)) * kTileBytes + v_off[j & 3] + (j >> 2) * 4096;
         const i16x4 lo = lds_read_tr16(p0);
         const i16x4 hi = lds_read_tr16(p0 + 2048);
         return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
@@ -374,7 +396,16 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
             mx = fmaxf(mx, s0[r]);
         }
     }
+    // Four steps per iteration: t is a multiple of 4 there, so every ring
+    // stage (u & 3) is a compile-time constant and the LDS addresses fold
+    // into the instructions' offsets.
     int t = 0;
+    for (; t + 3 < tiles; t += 4) {
+        step(t, s0, s1, mx, ka, w0, idk, idv);
+        step(t + 1, s1, s0, mx, ka, w0, idk, idv);
+        step(t + 2, s0, s1, mx, ka, w0, idk, idv);
+        step(t + 3, s1, s0, mx, ka, w0, idk, idv);
+    }
     for (; t + 1 < tiles; t += 2) {
         step(t, s0, s1, mx, ka, w0, idk, idv);
         step(t + 1, s1, s0, mx, ka, w0, idk, idv);
@@ -397,6 +428,30 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
                 *reinterpret_cast<u32x2*>(orow + 32 * dt + 8 * g + 4 * half) = pk;
             }
         if (lse != nullptr && half == 0) lse[bh * n + qrow_index] = m_run + log2f(l_tot);
+    }
+}
+
+// V [bh, n_kv, 128] -> KV4-transposed [bh, n_kv/4, 128, 4]: page j holds, for
+// each dim d, keys 4j..4j+3 (8 bytes). One thread per (page, 8 dims): four
+// 16-byte row reads, four 16-byte writes (64 contiguous bytes).
+__global__ __launch_bounds__(256) void kv4_transpose_kernel(const uint32_t* __restrict__ v, int64_t pages,
+                                                            uint32_t* __restrict__ vt) {
+    const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t page = idx >> 4;
+    const int c = static_cast<int>(idx & 15);
+    if (page >= pages) return;
+    u32x4 in[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) in[r] = reinterpret_cast<const u32x4*>(v + (page * 4 + r) * 64)[c];
+    u32x4* dst = reinterpret_cast<u32x4*>(vt + page * 256 + c * 16);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        // dims 8c + 2m (low halves of word m) and 8c + 2m + 1 (high halves)
+        const u32x4 o = {__builtin_amdgcn_perm(in[1][m], in[0][m], 0x05040100u),
+                         __builtin_amdgcn_perm(in[3][m], in[2][m], 0x05040100u),
+                         __builtin_amdgcn_perm(in[1][m], in[0][m], 0x07060302u),
+                         __builtin_amdgcn_perm(in[3][m], in[2][m], 0x07060302u)};
+        dst[m] = o;
     }
 }
 
@@ -453,6 +508,15 @@ int launch_merge(const void* oa, const float* sa, const void* ob, const float* s
     return check_launch("merge_kernel");
 }
 
+int launch_kv4_transpose(const void* v, int64_t bh, int64_t n_kv, void* vt, hipStream_t stream) {
+    const int64_t pages = bh * (n_kv / kKvBlock);
+    if (pages == 0) return 0;
+    const int64_t threads = pages * 16;
+    hipLaunchKernelGGL(kv4_transpose_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, stream,
+                       static_cast<const uint32_t*>(v), pages, static_cast<uint32_t*>(vt));
+    return check_launch("kv4_transpose_kernel");
+}
+
 int launch_remap_ids(const int32_t* ids, int64_t count, const int32_t* map, int64_t map_len, int32_t* out,
                      hipStream_t stream) {
     if (count == 0) return 0;
@@ -462,7 +526,7 @@ int launch_remap_ids(const int32_t* ids, int64_t count, const int32_t* map, int6
     return check_launch("remap_ids_kernel");
 }
 
-int launch_prefill(const void* q, const void* k, const void* v, int64_t bh, int64_t n, int64_t n_kv,
+int launch_prefill(const void* q, const void* k, const void* v, bool v_kv4t, int64_t bh, int64_t n, int64_t n_kv,
                    const int32_t* ids, const float* logw, int64_t samples, void* out, float* lse,
                    const int32_t* order, hipStream_t stream) {
     const int64_t qb = (n + kQueryBlock - 1) / kQueryBlock;
@@ -477,12 +541,15 @@ int launch_prefill(const void* q, const void* k, const void* v, int64_t bh, int6
     const int64_t per_xcd = (qb + 7) / 8;
     static bool attr_set = false;
     if (!attr_set) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_kernel),
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_kernel<false>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_kernel<true>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
         attr_set = true;
     }
     if (rows == 0) return 0;
-    hipLaunchKernelGGL(prefill_kernel, dim3(static_cast<unsigned>(per_xcd * 8 * bh)), dim3(kPfThreads), kLdsBytes,
+    auto kernel = v_kv4t ? prefill_kernel<true> : prefill_kernel<false>;
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(per_xcd * 8 * bh)), dim3(kPfThreads), kLdsBytes,
                        stream, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                        static_cast<const uint16_t*>(v), ids, logw, static_cast<uint16_t*>(out), lse, n, n_kv, qb, rows,
                        static_cast<int>(n_kv / kKvBlock), static_cast<int>(samples), scale_log2, order);

@@ -141,13 +141,23 @@ def main() -> int:
     samples = cfg.sample_pages * 32
     rows, fb, f_pre, b_sel = work_figures(bh, n, samples)
 
+    def prefill_inputs(plan):
+        """(ids, weights, order) that apply_plan hands to the prefill kernel."""
+        return plan.descriptor.reshape(rows, samples), plan.log_weights.reshape(rows, samples), None
+
     if cfg.cube_layout:
         # c4: the cube token layout computed in place on raster-order tensors
         # (same results as permuting Q/K/V, attending and permuting back).
-        from ab_attention.video import apply_cube_plan, cube_plan
+        from ab_attention.paged import _remap_ids
+        from ab_attention.video import _cube_maps, apply_cube_plan, cube_plan
 
         build_plan = lambda q_, k_, **kw: cube_plan(q_, k_, cfg.grid, **kw)  # noqa: E731
         apply_plan = lambda q_, k_, v_, plan_: apply_cube_plan(q_, k_, v_, plan_, cfg.grid)  # noqa: E731
+
+        def prefill_inputs(plan):  # noqa: F811
+            order, page_map = _cube_maps(cfg.grid, q.device)
+            return (_remap_ids(plan.descriptor.reshape(rows, samples), page_map),
+                    plan.log_weights.reshape(rows, samples), order)
 
     def step():
         plan = build_plan(q, k, sample_pages=cfg.sample_pages, seed=42)
@@ -162,17 +172,21 @@ def main() -> int:
     torch.cuda.synchronize()
     ms_call = (time.perf_counter() - t0) * 1e3 / args.steps
 
-    # Breakdown with HIP events on the launch stream (torch's current stream).
+    # Breakdown with HIP events on the launch stream (torch's current stream,
+    # which every launch of the library uses): build_plan (selection) and the
+    # prefill kernel alone (one launch).
+    from ab_attention.paged import _prefill
+
     stream = torch.cuda.current_stream()
-    plan = build_plan(q, k, sample_pages=cfg.sample_pages, seed=42)
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
     sel_ms, pre_ms = [], []
     for _ in range(max(3, args.steps)):
         ev[0].record(stream)
         plan = build_plan(q, k, sample_pages=cfg.sample_pages, seed=42)
         ev[1].record(stream)
+        ids, weights, order = prefill_inputs(plan)
         ev[2].record(stream)
-        apply_plan(q, k, v, plan)
+        _prefill(q, k, v, ids, weights, order, False)
         ev[3].record(stream)
         torch.cuda.synchronize()
         sel_ms.append(ev[0].elapsed_time(ev[1]))

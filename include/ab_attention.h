@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define AB_ABI_VERSION 1
+#define AB_ABI_VERSION 2
 
 enum ab_status {
     AB_OK = 0,
@@ -96,6 +96,21 @@ int ab_paged_prefill(const void *q, const void *k, const void *v, int64_t batch_
 int ab_paged_prefill_kv(const void *q, const void *k, const void *v, int64_t batch_heads, int64_t q_tokens,
                         int64_t kv_tokens, const int32_t *ids, const float *log_weights, int64_t samples,
                         void *out, float *lse, void *stream);
+
+/* ---- KV4-transposed V (the prefill's fast V layout) -------------------------
+ * No counterpart in the reference: FlashInfer reads V as [pages, 4, 1, 128]
+ * (ab_attention/flashinfer_backend.py:219-230). ab_kv4_transpose writes v bf16
+ * [batch_heads, kv_tokens, 128] (kv_tokens divisible by 4) as v_kv4t bf16
+ * [batch_heads, kv_tokens / 4, 128, 4]: page j holds, for each dim, keys
+ * 4j..4j+3. Same size as v; buffers 16-byte aligned.
+ * ab_paged_prefill_kv4t is ab_paged_prefill_kv over that layout, with an
+ * optional token order (NULL: identity; otherwise as ab_paged_prefill_ordered,
+ * order int32 [q_tokens]). It produces bit-identical results to the row-major
+ * entry points on the same inputs. */
+int ab_kv4_transpose(const void *v, int64_t batch_heads, int64_t kv_tokens, void *v_kv4t, void *stream);
+int ab_paged_prefill_kv4t(const void *q, const void *k, const void *v_kv4t, const int32_t *order,
+                          int64_t batch_heads, int64_t q_tokens, int64_t kv_tokens, const int32_t *ids,
+                          const float *log_weights, int64_t samples, void *out, float *lse, void *stream);
 
 /* ---- Attention-state merge -------------------------------------------------
  * Replaces FlashInfer's merge_state as used by _merge
