@@ -102,22 +102,76 @@ __global__ __launch_bounds__(kClusterThreads) void cluster_pool_kernel(
     const int valid = static_cast<int>(min<int64_t>(kQueryBlock, n - base));
     const int64_t row = bh * qb + blk;
 
-    // Token t of the head is row src_row(t) of Q and K: t itself, or order[t]
-    // for a permuted token layout (clamped into the head).
-    auto src_row = [&](int64_t t) -> int64_t {
-        return order ? min<int64_t>(max(order[t], 0), n - 1) : t;
-    };
-    // Stage the query block (zero rows past the sequence end).
+    // Every global load of the workgroup is issued at once, before any is
+    // used: thread tid loads 16 bytes of query rows tid/16 + 8i (i < 16) and
+    // of the key pairs tid/16 + 8i (i < 8), so the block costs one memory
+    // round trip instead of one per row group. Rows past the sequence end
+    // read as zero (queries) or are skipped (keys).
     const u32x4* qhead = reinterpret_cast<const u32x4*>(q + bh * n * kHeadDim);
-    for (int idx = tid; idx < kQueryBlock * 16; idx += kClusterThreads) {
-        const int r = idx >> 4, c = idx & 15;
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (r < valid) v = qhead[src_row(base + r) * 16 + c];
-        uint32_t* dst = block + r * kRowWords + c * 4;
-        dst[0] = v.x;
-        dst[1] = v.y;
-        dst[2] = v.z;
-        dst[3] = v.w;
+    const u32x4* khead = reinterpret_cast<const u32x4*>(k + bh * n * kHeadDim);
+    const int c16 = tid & 15, r0 = tid >> 4;
+    const int pairs = valid / 2;
+    // Token t of the head is stored row t, or order[t] for a permuted token
+    // layout (clamped into the head). Stored rows of query row r0 + 8i and of
+    // key rows 2p + (i & 1), p = r0 + 8(i/2); rows past the sequence end are
+    // clamped (their loads are discarded), and every order entry is loaded
+    // before any data load.
+    int64_t srow[16];
+    if (order) {
+        int32_t o[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[i] = order[base + min(r0 + 8 * i, valid - 1)];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) srow[i] = min<int64_t>(max(o[i], 0), n - 1);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) srow[i] = base + min(r0 + 8 * i, valid - 1);
+    }
+    int64_t krow[16];
+    if (order) {
+        int32_t o[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[i] = order[base + min(2 * (r0 + 8 * (i >> 1)) + (i & 1), valid - 1)];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) krow[i] = min<int64_t>(max(o[i], 0), n - 1);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) krow[i] = base + min(2 * (r0 + 8 * (i >> 1)) + (i & 1), valid - 1);
+    }
+    u32x4 qv[16], ka[8], kb[8];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) qv[i] = qhead[srow[i] * 16 + c16];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        ka[i] = khead[krow[2 * i] * 16 + c16];
+        kb[i] = khead[krow[2 * i + 1] * 16 + c16];
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        if (r0 + 8 * i >= valid) qv[i] = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        uint32_t* dst = block + (r0 + 8 * i) * kRowWords + c16 * 4;
+        dst[0] = qv[i].x;
+        dst[1] = qv[i].y;
+        dst[2] = qv[i].z;
+        dst[3] = qv[i].w;
+    }
+    // Pool the same tokens' keys: bf16(0.5 * (k_2r + k_2r+1)) (:244-266).
+    u32x4* kdst = reinterpret_cast<u32x4*>(pooled + (bh * (n / 2) + base / 2) * kHeadDim);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int p = r0 + 8 * i;
+        if (p < pairs) {
+            u32x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float lo = 0.5f * (bf16_lo(ka[i][e]) + bf16_lo(kb[i][e]));
+                const float hi = 0.5f * (bf16_hi(ka[i][e]) + bf16_hi(kb[i][e]));
+                o[e] = pack_bf16(lo, hi);
+            }
+            kdst[p * 16 + c16] = o;
+        }
     }
     __syncthreads();
 
@@ -213,23 +267,6 @@ __global__ __launch_bounds__(kClusterThreads) void cluster_pool_kernel(
         }
     }
 
-    // Pool the same tokens' keys: bf16(0.5 * (k_2r + k_2r+1)) (:244-266).
-    const u32x4* khead = reinterpret_cast<const u32x4*>(k + bh * n * kHeadDim);
-    u32x4* kdst = reinterpret_cast<u32x4*>(pooled + (bh * (n / 2) + base / 2) * kHeadDim);
-    const int pairs = valid / 2;
-    for (int idx = tid; idx < pairs * 16; idx += kClusterThreads) {
-        const int p = idx >> 4, c = idx & 15;
-        const u32x4 a = khead[src_row(base + 2 * p) * 16 + c];
-        const u32x4 b = khead[src_row(base + 2 * p + 1) * 16 + c];
-        u32x4 o;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float lo = 0.5f * (bf16_lo(a[e]) + bf16_lo(b[e]));
-            const float hi = 0.5f * (bf16_hi(a[e]) + bf16_hi(b[e]));
-            o[e] = pack_bf16(lo, hi);
-        }
-        kdst[p * 16 + c] = o;
-    }
 }
 
 // ---------------------------------------------------------------------------
