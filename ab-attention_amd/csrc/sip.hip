@@ -116,15 +116,31 @@ struct SipShared {
 
 // Thread-strided partial (sum, max) over the non-certain masses: thread t
 // folds i = t, t+256, ... in order (sip.cu:63-71). The kUnroll loads of a
-// step are issued together (clamped indices), then folded.
-template <class R>
+// step are issued together (clamped indices), then folded. With
+// kNoCertain (the first pass, before any block is marked) steps that lie
+// wholly inside the row need no per-element tests: every element is added.
+template <bool kNoCertain, class R>
 __device__ __forceinline__ void strided_partials(const R& rv, int pop, double& sum, double& mx) {
     const int t = threadIdx.x;
     sum = 0.0;
     // The maximum is order free: kept as the bit pattern of the largest
     // (positive) clamped mass, converted once at the end.
     uint32_t top = 0u;
-    for (int i0 = t; i0 < pop; i0 += kSipThreads * kUnroll) {
+    int i0 = t;
+    if (kNoCertain) {
+        for (; i0 + (kUnroll - 1) * kSipThreads < pop; i0 += kSipThreads * kUnroll) {
+            float r[kUnroll];
+#pragma unroll
+            for (int e = 0; e < kUnroll; ++e) r[e] = rv.raw(i0 + e * kSipThreads);
+#pragma unroll
+            for (int e = 0; e < kUnroll; ++e) {
+                const float x = R::x_of(r[e]);
+                sum = sum + static_cast<double>(x);
+                top = max(top, __float_as_uint(x));
+            }
+        }
+    }
+    for (; i0 < pop; i0 += kSipThreads * kUnroll) {
         float r[kUnroll];
 #pragma unroll
         for (int e = 0; e < kUnroll; ++e) r[e] = rv.raw(min(i0 + e * kSipThreads, pop - 1));
@@ -157,7 +173,7 @@ __device__ __forceinline__ void sip_row(R& rv, double sum, double mx, double* pr
     double scale;
     for (int pass = 0;; ++pass) {
         if (logical) {
-            if (pass > 0) strided_partials(rv, pop, sum, mx);
+            if (pass > 0) strided_partials<false>(rv, pop, sum, mx);
 #pragma unroll
             for (int off = 1; off < 32; off <<= 1) {
                 const double os = __shfl_down(sum, off, 32);
@@ -250,9 +266,21 @@ __device__ __forceinline__ void sip_row(R& rv, double sum, double mx, double* pr
     // A chunk starts at a multiple of 4; its masses are fetched 8 at a time.
     // Positions past the chunk and certain blocks add 0.0, which leaves the
     // (non-negative) running sum unchanged.
+    // Without certain blocks, groups of 8 wholly inside the chunk add every
+    // element (no tests).
     if (logical) {
         double chunk_mass = 0.0;
-        for (int i0 = begin; i0 < end; i0 += 8) {
+        int i0 = begin;
+        if (certainty == 0) {
+            for (; i0 + 8 <= end; i0 += 8) {
+                float r[8];
+                rv.raw8(i0, r);
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    chunk_mass = chunk_mass + static_cast<double>(R::x_of(r[e])) * scale;
+            }
+        }
+        for (; i0 < end; i0 += 8) {
             float r[8];
             rv.raw8(i0, r);
 #pragma unroll
@@ -292,7 +320,21 @@ __device__ __forceinline__ void sip_row(R& rv, double sum, double mx, double* pr
     if (t == 0) prefix[buckets] = static_cast<double>(residuals);
     if (logical) {
         double cumulative = sh.part[t];
-        for (int i0 = begin; i0 < end; i0 += 8) {
+        int i0 = begin;
+        if (certainty == 0) {
+            // No certain blocks: last = pop - 1, so no bucket start lies past
+            // it, and every element of a whole group of 8 is added.
+            for (; i0 + 8 <= end; i0 += 8) {
+                float r[8];
+                rv.raw8(i0, r);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    if (e % kBucket == 0) prefix[(i0 + e) / kBucket] = cumulative;
+                    cumulative = cumulative + static_cast<double>(R::x_of(r[e])) * scale;
+                }
+            }
+        }
+        for (; i0 < end; i0 += 8) {
             float r[8];
             rv.raw8(i0, r);
 #pragma unroll
@@ -424,7 +466,7 @@ __global__ __launch_bounds__(kSipWorkers) void sip_lds_kernel(
         lds_barrier();  // this row is staged
         LdsRow rv{values};
         double sum = 0.0, mx = 0.0;
-        if (t < kSipThreads) strided_partials(rv, pop, sum, mx);
+        if (t < kSipThreads) strided_partials<true>(rv, pop, sum, mx);
         sip_row(rv, sum, mx, prefix, sh, offsets[row], ids + row * int64_t(samples),
                 logw + row * int64_t(samples), pop, samples, [&] {
                     if (following < rows) stage();
@@ -446,7 +488,7 @@ __global__ __launch_bounds__(kSipWorkers) void sip_global_kernel(
     for (int w = t; w < (pop + 31) / 32; w += kSipWorkers) rv.marks[w] = 0u;
     lds_barrier();
     double sum = 0.0, mx = 0.0;
-    if (t < kSipThreads) strided_partials(rv, pop, sum, mx);
+    if (t < kSipThreads) strided_partials<true>(rv, pop, sum, mx);
     sip_row(rv, sum, mx, prefix, sh, offsets[row], ids + row * int64_t(samples), logw + row * int64_t(samples),
             pop, samples, [] {});
 }
