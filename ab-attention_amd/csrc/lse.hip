@@ -230,9 +230,13 @@ __global__ __launch_bounds__(kLseThreads, 3) void lse_kernel(
             const int R = (tid >> 3) + 32 * h2, U = tid & 7;
             const int64_t qbk = qgroup * kLseQBlocks + R / kCentroids;
             const u32x4 val = *reinterpret_cast<const u32x4*>(ostage + R * 128 + 16 * (U ^ ((R >> 1) & 7)));
+            // Streaming store: the pair-LSEs are read back only by the next
+            // kernel, and allocating them in the caches would evict the
+            // pooled keys that every workgroup of the head re-reads.
             if (qbk < qb)
-                *reinterpret_cast<u32x4*>(lse + ((bh * qb + qbk) * kCentroids + R % kCentroids) * ld +
-                                          64 * j + 8 * U) = val;
+                __builtin_nontemporal_store(
+                    val, reinterpret_cast<u32x4*>(lse + ((bh * qb + qbk) * kCentroids + R % kCentroids) * ld +
+                                                  64 * j + 8 * U));
         }
     };
 
