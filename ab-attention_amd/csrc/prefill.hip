@@ -113,9 +113,17 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
     // order: at any time all XCDs work on the same head (its K/V stay in the
     // shared last-level cache), each on a contiguous eighth of its query
     // blocks (neighbouring blocks share most sampled pages in the XCD's L2).
+    // Within an XCD, slots s and s + 32 of each full generation of 64 slots
+    // run on the same CU (two workgroups per CU), so they take adjacent
+    // query blocks: their sampled pages overlap and they sweep them in step,
+    // which turns part of the gathers into L1 hits.
     const int64_t hw = blockIdx.x;
-    const int64_t xcd = hw & 7, slot = hw >> 3;
+    const int64_t xcd = hw & 7, slot0 = hw >> 3;
     const int64_t per_xcd = (qb + 7) / 8;
+    const int64_t generation = slot0 >> 6, s64 = slot0 & 63;
+    const int64_t slot = (generation + 1) * 64 <= per_xcd * (rows / qb)
+                             ? generation * 64 + 2 * (s64 & 31) + (s64 >> 5)
+                             : slot0;
     const int64_t bh = slot / per_xcd;
     const int64_t blk = xcd * per_xcd + slot % per_xcd;
     if (bh >= rows / qb || blk >= qb) return;

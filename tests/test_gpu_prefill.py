@@ -118,3 +118,19 @@ def test_prefill_c1_head_subset(oracle_mod):
         e = np.abs(got[lo:hi] - ref_o[0, lo:hi])
         assert e.max() <= MAX_ABS, (r, e.max())
         assert np.abs(got_lse[lo:hi] - ref_lse[0, lo:hi]).max() <= LSE_ABS
+
+
+def test_prefill_workgroup_generations(oracle_mod):
+    """7 heads x 80 query blocks: each XCD runs 70 row slots, one full
+    generation of 64 (where the two workgroups sharing a CU take adjacent
+    query blocks) and a partial one. Every row must be computed once: the
+    output starts as NaN and all rows are checked against the oracle."""
+    rng = np.random.default_rng(21)
+    torch.manual_seed(4)
+    heads, n, samples = 7, 80 * 128, 32
+    print(f"prefill generations heads={heads} n={n}", flush=True)
+    q, k, v = (torch.randn(1, heads, n, 128).to(torch.bfloat16) for _ in range(3))
+    rows, fb = heads * (n // 128), n // 4
+    ids = np.sort(rng.choice(fb, size=(rows, samples), replace=True), axis=1).astype(np.int32)
+    logw = (rng.random((rows, samples)) * 3).astype(np.float32)
+    _check(q, k, v, ids, logw, oracle_mod)
