@@ -38,6 +38,8 @@ SIGNATURES = {
     "ab_remap_ids": (ctypes.c_int, [_P, _I64, _P, _I64, _P, _P]),
     "ab_paged_prefill_ordered": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _P, _P, _I64, _P, _P, _P]),
     "ab_kv4_transpose": (ctypes.c_int, [_P, _I64, _I64, _P, _P]),
+    "ab_ibcs_sip_workspace_bytes": (_SZ, [_I64, _I64]),
+    "ab_ibcs_sip": (ctypes.c_int, [_P, _P, _P, _I64, _I64, _P, _I64, _P, _SZ, _P, _P, _P]),
     "ab_paged_prefill_kv4t": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _P, _P, _P]),
 }
 

@@ -53,13 +53,12 @@ def build_plan(q, k, *, sample_pages=64, seed=42):
     Returns a ``SamplePlan`` with both tensors shaped [rows, pages, 32].
     (Reference: attention.py:26-82.)
     """
-    from . import _C as ops
-
-    return _build_plan(q, k, sample_pages, seed, ops.ibcs)
+    return _build_plan(q, k, sample_pages, seed)
 
 
-def _build_plan(q, k, sample_pages, seed, ibcs):
-    """build_plan with the scoring step ``ibcs(q_chunk, k_chunk) -> scores``."""
+def _build_plan(q, k, sample_pages, seed, order=None):
+    """build_plan, with the tokens read through ``order`` (int32 [tokens])
+    when it is given (the cube layout on stored-order tensors)."""
     sample_pages = int(sample_pages)
     if q.ndim != 4 or q.shape != k.shape or q.shape[2] % 4:
         raise ValueError("Q/K must match [B,H,N,D] with N divisible by 4")
@@ -87,12 +86,13 @@ def _build_plan(q, k, sample_pages, seed, ibcs):
     for start in range(0, batch_heads, heads_per_chunk):
         stop = min(batch_heads, start + heads_per_chunk)
         first, last = start * q_blocks, stop * q_blocks
-        scores = ibcs(
+        # IBCS scores and SIP sampling of the chunk (the reference's _C.ibcs
+        # then _C.sip) in one native call that keeps the scores on chip.
+        ops.ibcs_sip(
             flat_q[start:stop].unsqueeze(0).contiguous(),
             flat_k[start:stop].unsqueeze(0).contiguous(),
+            offsets[first:last], sampled[first:last], log_weights[first:last], order,
         )
-        ops.sip(scores, offsets[first:last], sampled[first:last], log_weights[first:last])
-        del scores
 
     return SamplePlan(
         sampled.reshape(rows, sample_pages, 32),

@@ -92,12 +92,11 @@ def cube_plan(q: torch.Tensor, k: torch.Tensor, grid, *, sample_pages: int = 64,
     kept in their stored (raster) order: equal to build_plan(q[:, :, order],
     k[:, :, order], ...) with ``order`` from cube_order(grid), without
     permuting q or k. The plan's ids are cube-order KV4 blocks."""
-    from . import _C
     from .attention import _build_plan
 
     _check_cube(q, grid)
     order, _ = _cube_maps(grid, q.device)
-    return _build_plan(q, k, sample_pages, seed, lambda qc, kc: _C.ibcs_ordered(qc, kc, order))
+    return _build_plan(q, k, sample_pages, seed, order)
 
 
 @torch.no_grad()

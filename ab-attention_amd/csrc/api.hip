@@ -23,6 +23,10 @@ int launch_masses(const void* lse, const float* pops, const float* lse_max, cons
 int launch_sip(const float* scores, const float* offsets, int64_t rows, int64_t population, int64_t samples,
                int32_t* ids, float* logw, hipStream_t stream);
 bool sip_fits(int64_t population);
+bool sip_fused_fits(int64_t population);
+int launch_sip_fused(const void* lse, const float* pops, const float* lse_max, const float* lse_den, int64_t ld,
+                     const float* offsets, int64_t rows, int64_t population, int64_t samples, int32_t* ids,
+                     float* logw, hipStream_t stream);
 int launch_prefill(const void* q, const void* k, const void* v, bool v_kv4t, int64_t bh, int64_t n, int64_t n_kv,
                    const int32_t* ids, const float* logw, int64_t samples, void* out, float* lse,
                    const int32_t* order, hipStream_t stream);
@@ -189,6 +193,48 @@ int ab_ibcs_ordered(const void* q, const void* k, const int32_t* order, int64_t 
                     void* workspace, size_t workspace_bytes, float* scores, void* stream) {
     if (!order) return set_error(AB_ERR_INVALID, "ibcs: null token order");
     return ibcs_chain(q, k, order, batch_heads, tokens, workspace, workspace_bytes, scores, stream);
+}
+
+size_t ab_ibcs_sip_workspace_bytes(int64_t batch_heads, int64_t tokens) {
+    if (batch_heads <= 0 || tokens <= 0 || tokens % kKvBlock) return 0;
+    const IbcsLayout L = ibcs_layout(batch_heads, tokens);
+    // Rows too large for the fused kernel's LDS go through scores in memory.
+    return sip_fused_fits(L.fb) ? L.total : L.total + align256(size_t(L.rows) * L.fb * 4);
+}
+
+int ab_ibcs_sip(const void* q, const void* k, const int32_t* order, int64_t batch_heads, int64_t tokens,
+                const float* offsets, int64_t samples, void* workspace, size_t workspace_bytes, int32_t* ids,
+                float* log_weights, void* stream) {
+    if (int rc = check_qk_shape("ibcs_sip", batch_heads, tokens)) return rc;
+    const IbcsLayout L = ibcs_layout(batch_heads, tokens);
+    if (!(samples > 0 && samples < L.fb))
+        return set_error(AB_ERR_INVALID, "ibcs_sip: sample count must be inside the population");
+    if (!sip_fits(L.fb)) return set_error(AB_ERR_INVALID, "ibcs_sip: population exceeds single-workgroup LDS capacity");
+    if (!q || !k || !offsets || !workspace || !ids || !log_weights)
+        return set_error(AB_ERR_INVALID, "ibcs_sip: null pointer");
+    if (!aligned16(q) || !aligned16(k)) return set_error(AB_ERR_INVALID, "ibcs_sip: q and k must be 16-byte aligned");
+    const size_t need = ab_ibcs_sip_workspace_bytes(batch_heads, tokens);
+    if (workspace_bytes < need)
+        return set_error(AB_ERR_INVALID, "ibcs_sip: workspace of %zu bytes is smaller than the %zu required",
+                         workspace_bytes, need);
+    if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+        return set_error(AB_ERR_INVALID, "ibcs_sip: workspace must be 256-byte aligned");
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    char* ws = static_cast<char*>(workspace);
+    float* pops = reinterpret_cast<float*>(ws + L.pops);
+    float* lse_max = reinterpret_cast<float*>(ws + L.lse_max);
+    float* lse_den = reinterpret_cast<float*>(ws + L.lse_den);
+    if (int rc = launch_cluster_pool(q, k, batch_heads, tokens, ws + L.centroids, pops, ws + L.pooled,
+                                     qk_scale_log2(), order, st))
+        return rc;
+    if (int rc = launch_lse(ws + L.centroids, ws + L.pooled, batch_heads, tokens, ws + L.lse, lse_max, lse_den, st))
+        return rc;
+    if (sip_fused_fits(L.fb))
+        return launch_sip_fused(ws + L.lse, pops, lse_max, lse_den, L.ld, offsets, L.rows, L.fb, samples, ids,
+                                log_weights, st);
+    float* scores = reinterpret_cast<float*>(ws + L.total);
+    if (int rc = launch_masses(ws + L.lse, pops, lse_max, lse_den, L.rows, L.fb, scores, st)) return rc;
+    return launch_sip(scores, offsets, L.rows, L.fb, samples, ids, log_weights, st);
 }
 
 int ab_sip(const float* scores, const float* offsets, int64_t rows, int64_t population, int64_t samples,

@@ -21,6 +21,7 @@
 #include <cfloat>
 
 #include "common.hpp"
+#include "masses.hpp"
 
 namespace ab {
 namespace {
@@ -280,46 +281,26 @@ __global__ __launch_bounds__(kMassThreads) void masses_kernel(
     const float* __restrict__ lse_max, const float* __restrict__ lse_den,
     float* __restrict__ scores, int fb, int64_t ld) {
     const int64_t row = blockIdx.x;
-    float weight[kCentroids], inv_den[kCentroids], mx[kCentroids];
-    float total = 0.0f;
-#pragma unroll
-    for (int s = 0; s < kCentroids; ++s) {
-        weight[s] = pops[row * kCentroids + s];
-        inv_den[s] = __fdiv_rn(1.0f, lse_den[row * kCentroids + s]);
-        mx[s] = lse_max[row * kCentroids + s];
-        total += weight[s];
-    }
-    const float inv_total = __fdiv_rn(1.0f, total);
+    RowMasses rm;
+    rm.load(pops, lse_max, lse_den, row);
     const _Float16* src = lse + row * kCentroids * ld;
     float* dst = scores + row * int64_t(fb);
-    typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
     for (int j0 = threadIdx.x * 8; j0 < fb; j0 += kMassThreads * 8) {
+        f16x8 h[kCentroids];
+#pragma unroll
+        for (int s = 0; s < kCentroids; ++s) h[s] = *reinterpret_cast<const f16x8*>(src + s * ld + j0);
         float score[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) score[e] = 0.0f;
-#pragma unroll
-        for (int s = 0; s < kCentroids; ++s) {
-            const f16x8 h = *reinterpret_cast<const f16x8*>(src + s * ld + j0);
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                score[e] = __builtin_fmaf(weight[s],
-                                          fast_exp2(static_cast<float>(h[e]) - mx[s]) * inv_den[s],
-                                          score[e]);
-        }
+        rm.eight(h, score);
         // Two 16-byte stores (rows start at any multiple of 4 bytes, which
         // global stores accept); the ragged end of the row element by element.
         typedef float f32x4_u __attribute__((ext_vector_type(4), aligned(4)));
         if (j0 + 8 <= fb) {
-            const f32x4_u lo = {score[0] * inv_total, score[1] * inv_total, score[2] * inv_total,
-                                score[3] * inv_total};
-            const f32x4_u hi = {score[4] * inv_total, score[5] * inv_total, score[6] * inv_total,
-                                score[7] * inv_total};
-            *reinterpret_cast<f32x4_u*>(dst + j0) = lo;
-            *reinterpret_cast<f32x4_u*>(dst + j0 + 4) = hi;
+            *reinterpret_cast<f32x4_u*>(dst + j0) = f32x4_u{score[0], score[1], score[2], score[3]};
+            *reinterpret_cast<f32x4_u*>(dst + j0 + 4) = f32x4_u{score[4], score[5], score[6], score[7]};
         } else {
 #pragma unroll
             for (int e = 0; e < 8; ++e)
-                if (j0 + e < fb) dst[j0 + e] = score[e] * inv_total;
+                if (j0 + e < fb) dst[j0 + e] = score[e];
         }
     }
 }

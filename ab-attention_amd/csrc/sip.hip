@@ -33,6 +33,7 @@
 #include <algorithm>
 
 #include "common.hpp"
+#include "masses.hpp"
 
 namespace ab {
 namespace {
@@ -474,6 +475,59 @@ __global__ __launch_bounds__(kSipWorkers) void sip_lds_kernel(
     }
 }
 
+// Fused masses + SIP for rows that fit in LDS: each persistent workgroup
+// computes its row's masses from the fp16 pair-LSEs [8, ld] straight into
+// LDS (RowMasses: the arithmetic of masses_kernel, so the same bits as the
+// scores that kernel writes), then samples the row as sip_lds_kernel does.
+// The scores never go to global memory. A row's pair-LSEs are loaded two
+// groups of 8 blocks per thread at a time (16 loads in flight).
+__global__ __launch_bounds__(kSipWorkers) void sip_fused_kernel(
+    const _Float16* __restrict__ lse, const float* __restrict__ pops, const float* __restrict__ lse_max,
+    const float* __restrict__ lse_den, int64_t ld, const float* __restrict__ offsets, int32_t* __restrict__ ids,
+    float* __restrict__ logw, int population, int samples, int64_t rows) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ SipShared sh;
+    const int t = threadIdx.x;
+    const int pop = population;
+    const int buckets = (pop + kBucket - 1) / kBucket;
+    const int groups = (pop + 7) / 8;
+    double* prefix = reinterpret_cast<double*>(smem);
+    float* values = reinterpret_cast<float*>(smem + sip_values_offset(buckets));
+    for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+        // The previous row's last reads of values[] finished before the
+        // barrier ahead of its stores, so the row can be written over.
+        RowMasses rm;
+        rm.load(pops, lse_max, lse_den, row);
+        const _Float16* src = lse + row * kCentroids * ld;
+        for (int g0 = t; g0 < groups; g0 += 2 * kSipWorkers) {
+            f16x8 h[2][kCentroids];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int g = min(g0 + u * kSipWorkers, groups - 1);
+#pragma unroll
+                for (int c = 0; c < kCentroids; ++c) h[u][c] = *reinterpret_cast<const f16x8*>(src + c * ld + 8 * g);
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int g = g0 + u * kSipWorkers;
+                if (g < groups) {
+                    float m[8];
+                    rm.eight(h[u], m);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        if (8 * g + e < pop) values[8 * g + e] = m[e] > 0.0f ? m[e] : 0.0f;  // NaN, negatives -> +0
+                }
+            }
+        }
+        lds_barrier();
+        LdsRow rv{values};
+        double sum = 0.0, mx = 0.0;
+        if (t < kSipThreads) strided_partials<true>(rv, pop, sum, mx);
+        sip_row(rv, sum, mx, prefix, sh, offsets[row], ids + row * int64_t(samples), logw + row * int64_t(samples),
+                pop, samples, [] {});
+    }
+}
+
 __global__ __launch_bounds__(kSipWorkers) void sip_global_kernel(
     const float* __restrict__ masses, const float* __restrict__ offsets, int32_t* __restrict__ ids,
     float* __restrict__ logw, int population, int samples) {
@@ -521,6 +575,29 @@ size_t sip_lds_bytes(int64_t population, bool lds_values) {
 }
 
 bool sip_fits(int64_t population) { return sip_lds_bytes(population, false) + kSipStaticLds <= kLdsLimit; }
+
+bool sip_fused_fits(int64_t population) { return sip_lds_bytes(population, true) + kSipStaticLds <= kLdsLimit; }
+
+int launch_sip_fused(const void* lse, const float* pops, const float* lse_max, const float* lse_den, int64_t ld,
+                     const float* offsets, int64_t rows, int64_t population, int64_t samples, int32_t* ids,
+                     float* logw, hipStream_t stream) {
+    if (!sip_fused_fits(population))
+        return set_error(1, "sip: population %lld does not fit the fused kernel's LDS", (long long)population);
+    if (rows == 0) return 0;
+    const size_t bytes = sip_lds_bytes(population, true);
+    const void* fn = reinterpret_cast<const void*>(sip_fused_kernel);
+    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+    int device = 0, cus = 0, per_cu = 0;
+    (void)hipGetDevice(&device);
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kSipWorkers, bytes) != hipSuccess || per_cu < 1)
+        per_cu = 1;
+    const int64_t grid = std::min<int64_t>(rows, int64_t(std::max(cus, 1)) * per_cu);
+    hipLaunchKernelGGL(sip_fused_kernel, dim3(static_cast<unsigned>(grid)), dim3(kSipWorkers), bytes, stream,
+                       static_cast<const _Float16*>(lse), pops, lse_max, lse_den, ld, offsets, ids, logw,
+                       static_cast<int>(population), static_cast<int>(samples), rows);
+    return check_launch("sip_fused_kernel");
+}
 
 int launch_sip(const float* scores, const float* offsets, int64_t rows, int64_t population, int64_t samples,
                int32_t* ids, float* logw, hipStream_t stream) {

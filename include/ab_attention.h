@@ -74,6 +74,20 @@ int ab_ibcs_masses(const void *block_lse, const float *populations, const float 
 int ab_sip(const float *scores, const float *offsets, int64_t rows, int64_t population, int64_t samples,
            int32_t *ids, float *log_weights, void *stream);
 
+/* ---- Fused plan: IBCS + SIP without materialised scores -------------------
+ * build_plan's per-chunk work (ab_attention/attention.py:65-75: _C.ibcs then
+ * _C.sip) in one call: q, k bf16 [batch_heads, tokens, 128] (tokens read
+ * through `order` when it is not NULL, as ab_ibcs_ordered), offsets f32
+ * [rows] -> ids int32 / log_weights f32 [rows, samples], the same bits as
+ * ab_ibcs followed by ab_sip. Rows whose masses fit in LDS are scored and
+ * sampled by one kernel that computes each row's masses straight into LDS;
+ * larger rows go through scores in the workspace. `workspace` is
+ * ab_ibcs_sip_workspace_bytes() bytes, 256-byte aligned. */
+size_t ab_ibcs_sip_workspace_bytes(int64_t batch_heads, int64_t tokens);
+int ab_ibcs_sip(const void *q, const void *k, const int32_t *order, int64_t batch_heads, int64_t tokens,
+                const float *offsets, int64_t samples, void *workspace, size_t workspace_bytes, int32_t *ids,
+                float *log_weights, void *stream);
+
 /* ---- Weighted paged prefill ------------------------------------------------
  * Replaces the FlashInfer FA3 run with the ABSipAttention variant
  * (ab_attention/flashinfer_backend.py:30-59, :164-242): q, k, v bf16

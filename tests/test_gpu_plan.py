@@ -1,0 +1,81 @@
+"""The fused plan (_C.ibcs_sip / ab_ibcs_sip, used by build_plan) against the
+reference-structured path (_C.ibcs then _C.sip, csrc/bindings.cpp:3-8):
+SIP ids and weights must be bit-identical, since the fused kernel computes
+each row's masses with the masses kernel's arithmetic straight into LDS."""
+import pytest
+import torch
+
+from ab_attention import _C, build_plan
+from ab_attention.synthetic import CONFIGS, make_qkv
+
+pytestmark = pytest.mark.gpu
+
+
+def _both(q, k, samples, order=None, seed=0):
+    b, h, n, _ = q.shape
+    rows = b * h * -(-n // 128)
+    offsets = torch.rand(rows, generator=torch.Generator().manual_seed(seed)).cuda()
+    ids_f = torch.empty(rows, samples, dtype=torch.int32, device="cuda")
+    w_f = torch.empty(rows, samples, dtype=torch.float32, device="cuda")
+    _C.ibcs_sip(q, k, offsets, ids_f, w_f, order)
+    scores = _C.ibcs(q, k) if order is None else _C.ibcs_ordered(q, k, order)
+    ids_s = torch.empty_like(ids_f)
+    w_s = torch.empty_like(w_f)
+    _C.sip(scores, offsets, ids_s, w_s)
+    torch.cuda.synchronize()
+    return ids_f, w_f, ids_s, w_s
+
+
+def _assert_same(ids_f, w_f, ids_s, w_s):
+    assert torch.equal(ids_f, ids_s)
+    assert torch.equal(w_f.view(torch.int32), w_s.view(torch.int32))
+
+
+@pytest.mark.parametrize("n,heads,samples", [(2048, 2, 64), (32760, 1, 2048), (1000, 3, 32)])
+def test_fused_plan_equals_ibcs_then_sip(n, heads, samples):
+    """c0, one full-length c1 head (8,190 blocks: a ragged last group of 8), a
+    ragged query block."""
+    print(f"fused plan n={n} heads={heads} samples={samples}", flush=True)
+    cfg = CONFIGS[1] if n == 32760 else CONFIGS[0]
+    if n == 32760:
+        q, k, _ = make_qkv(cfg, heads=[0], dtype=torch.bfloat16)
+        q, k = q[:1], k[:1]
+    else:
+        torch.manual_seed(n + heads)
+        q, k = (torch.randn(1, heads, n, 128).to(torch.bfloat16) for _ in range(2))
+    _assert_same(*_both(q.cuda().contiguous(), k.cuda().contiguous(), samples))
+
+
+def test_fused_plan_ordered():
+    """Tokens read through a permutation (the cube layout's path)."""
+    print("fused plan ordered n=4096", flush=True)
+    torch.manual_seed(3)
+    n = 4096
+    q, k = (torch.randn(1, 2, n, 128).to(torch.bfloat16).cuda() for _ in range(2))
+    order = torch.randperm(n, generator=torch.Generator().manual_seed(5)).to(torch.int32).cuda()
+    _assert_same(*_both(q, k, 256, order=order, seed=1))
+
+
+def test_fused_plan_large_rows_fallback():
+    """27,000 blocks per row do not fit the fused kernel's LDS: the masses go
+    through memory (masses kernel, then the global-memory SIP kernel)."""
+    print("fused plan fallback n=108000", flush=True)
+    torch.manual_seed(8)
+    n = 108000
+    q, k = (torch.randn(1, 1, n, 128).to(torch.bfloat16).cuda() for _ in range(2))
+    _assert_same(*_both(q, k, 2048, seed=2))
+
+
+def test_build_plan_uses_fused_path():
+    """build_plan's plan equals the reference-structured path's on the same uniforms."""
+    print("build_plan vs ibcs+sip", flush=True)
+    q, k, _ = make_qkv(CONFIGS[0], dtype=torch.bfloat16)
+    q, k = q.cuda(), k.cuda()
+    plan = build_plan(q, k, sample_pages=2, seed=42)
+    rows = plan.descriptor.shape[0]
+    offsets = torch.rand(rows, device=q.device, generator=torch.Generator(q.device).manual_seed(42))
+    ids = torch.empty(rows, 64, dtype=torch.int32, device=q.device)
+    w = torch.empty(rows, 64, dtype=torch.float32, device=q.device)
+    _C.sip(_C.ibcs(q, k), offsets, ids, w)
+    torch.cuda.synchronize()
+    _assert_same(plan.descriptor.reshape(rows, 64), plan.log_weights.reshape(rows, 64), ids, w)
