@@ -73,6 +73,18 @@ __device__ __forceinline__ void lds_dma16_after_reads(const void* base, uint32_t
 }
 #pragma clang diagnostic pop
 
+// (float)half - ref for the low (kHigh = false) or high half of a packed
+// fp16 pair, in one v_fma_mix_f32: half * 1.0 + (-ref), rounded once.
+template <bool kHigh>
+__device__ __forceinline__ float f16_minus(uint32_t packed, float ref) {
+    float r;
+    if (kHigh)
+        asm("v_fma_mix_f32 %0, %1, 1.0, -%2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(packed), "v"(ref));
+    else
+        asm("v_fma_mix_f32 %0, %1, 1.0, -%2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(packed), "v"(ref));
+    return r;
+}
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
@@ -132,7 +144,27 @@ __global__ __launch_bounds__(kLseThreads, 3) void lse_kernel(
     // (= 2*col + rep) holds its 16-byte chunk k at position k ^ (p/2 % 16);
     // rows past the head's end re-read its last row (never used).
     const int last_row = 2 * fb - 1;
+    // Chunks wholly inside the head use a wave-uniform chunk base and the
+    // lane's fixed offsets (no per-transfer address arithmetic); only the
+    // head's last chunk clamps its rows.
+    uint32_t chunk_off[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int p = 4 * k + (lane >> 4);
+        chunk_off[k] = uint32_t(p) * 256u + 16u * uint32_t((lane & 15) ^ ((p >> 1) & 15));
+    }
     auto issue_chunk = [&](int c) {
+        if ((c + 1) * kLseChunk * kReps <= last_row + 1) {
+            const uint16_t* base = keys + int64_t(c) * kLseChunk * kReps * kHeadDim;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                if (k == 0)
+                    lds_dma16_after_reads(base, chunk_off[k], in_base + k * 1024);
+                else
+                    lds_dma16(base, chunk_off[k], in_base + k * 1024);
+            }
+            return;
+        }
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const int p = 4 * k + (lane >> 4);
@@ -194,27 +226,44 @@ __global__ __launch_bounds__(kLseThreads, 3) void lse_kernel(
             }
             const f16x2 h01 = __builtin_convertvector(f32x2{l[0], l[1]}, f16x2);
             const f16x2 h23 = __builtin_convertvector(f32x2{l[2], l[3]}, f16x2);
-            float f[4] = {static_cast<float>(h01[0]), static_cast<float>(h01[1]), static_cast<float>(h23[0]),
-                          static_cast<float>(h23[1])};
-            if (kTail) {
-#pragma unroll
-                for (int v = 0; v < 4; ++v)
-                    if (jq + v >= fb) f[v] = -INFINITY;
-            }
             const u32x2 packed = {__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23)};
             const int R = 16 * rt + col, u = 4 * wave + quad;  // 8-byte unit of the round row
             *reinterpret_cast<u32x2*>(ostage + R * 128 + 16 * ((u >> 1) ^ ((R >> 1) & 7)) + 8 * (u & 1)) = packed;
 
-            const float tmax = fmaxf(fmaxf(f[0], f[1]), fmaxf(f[2], f[3]));
-            top[rt] = fmaxf(top[rt], tmax);
-            const bool grow = tmax > ref[rt] + kLseSlack;
-            if (__any(grow)) {
-                const float nr = grow ? tmax : ref[rt];
-                den[rt] *= fast_exp2(ref[rt] - nr);
-                ref[rt] = nr;
-            }
+            if (kTail) {
+                float f[4] = {static_cast<float>(h01[0]), static_cast<float>(h01[1]), static_cast<float>(h23[0]),
+                              static_cast<float>(h23[1])};
 #pragma unroll
-            for (int v = 0; v < 4; ++v) den[rt] += fast_exp2(f[v] - ref[rt]);
+                for (int v = 0; v < 4; ++v)
+                    if (jq + v >= fb) f[v] = -INFINITY;
+                const float tmax = fmaxf(fmaxf(f[0], f[1]), fmaxf(f[2], f[3]));
+                top[rt] = fmaxf(top[rt], tmax);
+                const bool grow = tmax > ref[rt] + kLseSlack;
+                if (__any(grow)) {
+                    const float nr = grow ? tmax : ref[rt];
+                    den[rt] *= fast_exp2(ref[rt] - nr);
+                    ref[rt] = nr;
+                }
+#pragma unroll
+                for (int v = 0; v < 4; ++v) den[rt] += fast_exp2(f[v] - ref[rt]);
+            } else {
+                // The maximum of the four fp16 values in fp16 (exact), and
+                // f - ref straight from the fp16 halves with v_fma_mix_f32
+                // (f16 -> f32 is exact, so this is the rounded f - ref).
+                const f16x2 m2 = __builtin_elementwise_max(h01, h23);
+                const float tmax = static_cast<float>(m2[0] > m2[1] ? m2[0] : m2[1]);
+                top[rt] = fmaxf(top[rt], tmax);
+                const bool grow = tmax > ref[rt] + kLseSlack;
+                if (__any(grow)) {
+                    const float nr = grow ? tmax : ref[rt];
+                    den[rt] *= fast_exp2(ref[rt] - nr);
+                    ref[rt] = nr;
+                }
+                den[rt] += fast_exp2(f16_minus<false>(packed[0], ref[rt]));
+                den[rt] += fast_exp2(f16_minus<true>(packed[0], ref[rt]));
+                den[rt] += fast_exp2(f16_minus<false>(packed[1], ref[rt]));
+                den[rt] += fast_exp2(f16_minus<true>(packed[1], ref[rt]));
+            }
         }
     };
 
