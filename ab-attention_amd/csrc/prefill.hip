@@ -62,6 +62,7 @@ static_assert(kLdsBytes * 2 <= 160 * 1024, "two workgroups per CU must fit in LD
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+typedef __attribute__((address_space(3))) const u32x4 lds_u32x4;
 typedef __attribute__((address_space(3))) unsigned char lds_u8;
 
 // Transposing LDS read: within each 16-lane group, lane i receives element
@@ -225,8 +226,17 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) v_off[dt] = half * 1024 + (2 * dt + gd) * 128 + 32 * (r ^ dt) + 8 * q4;
     }
+    // The same as absolute LDS addresses, so every operand read is one
+    // register plus the instruction's constant offset (the dynamic-LDS base
+    // is not a compile-time constant and would cost an add per read).
+    uint32_t k_abs[8], v_abs[4];
+#pragma unroll
+    for (int s8 = 0; s8 < 8; ++s8) k_abs[s8] = lds0 + kKRing + k_off[s8];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) v_abs[dt] = lds0 + kVRing + v_off[dt];
     auto read_k = [&](int u, int j) {
-        return *reinterpret_cast<const u32x4*>(smem + kKRing + (u & (kRing - 1)) * kTileBytes + k_off[j]);
+        return *reinterpret_cast<const lds_u32x4*>(
+            static_cast<uintptr_t>(k_abs[j] + (u & (kRing - 1)) * kTileBytes));
     };
     // PV A operand j of tile u: V^T for k-step j/4, dims 32(j%4) .. +31. MFMA
     // k-index 8*half + 4t + r of k-step ks is key r of tile page 4*ks + 2t +
@@ -247,9 +257,10 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
             const u32x2 hi = *reinterpret_cast<const u32x2*>(smem + vt1 + off);
             return __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
         }
-        const unsigned char* p0 = smem + kVRing + (u & (kRing - 1)) * kTileBytes + v_off[j & 3] + (j >> 2) * 4096;
-        const i16x4 lo = lds_read_tr16(p0);
-        const i16x4 hi = lds_read_tr16(p0 + 2048);
+        const uint32_t a0 = v_abs[j & 3] + (u & (kRing - 1)) * kTileBytes + (j >> 2) * 4096;
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_i16x4*>(static_cast<uintptr_t>(a0)));
+        const i16x4 hi =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_i16x4*>(static_cast<uintptr_t>(a0 + 2048)));
         return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
     };
 
@@ -310,8 +321,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
         for (int j = 0; j < 8; ++j) {
             sn = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ka[j]), bq[j], sn, 0, 0, 0);
             const float p0 = fast_exp2(sc[2 * j]), p1 = fast_exp2(sc[2 * j + 1]);
-            psum += p0;
-            psum += p1;
+            psum = j == 0 ? p0 + p1 : (psum + p0) + p1;
             pw[j >> 1][j & 1] = pack_bf16(p0, p1);
             va[j] = read_v(t, j);
             if (j == 1) dma_k(t + 5, idk[0], 0);
@@ -338,7 +348,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
             const float y1 = __builtin_fmaf(sn[2 * j + 1], scale_log2, wm[j >> 1]);
             sn[2 * j] = y0;
             sn[2 * j + 1] = y1;
-            mx = fmaxf(mx, fmaxf(y0, y1));
+            mx = fmaxf(fmaxf(mx, y0), y1);  // one v_max3_f32
             if (j == 6) idk = load_ids(t + 6);
             if (j == 7) idv = load_ids(t + 4);
             __builtin_amdgcn_sched_barrier(0);
