@@ -9,7 +9,9 @@
 // reference's max(sum, 1e-20) floor never binds for finite inputs (sum >= 1).
 // D is accumulated from the fp16-rounded values against a lazily moved
 // reference and rebased on the exact maximum at the end, which matches the
-// reference up to fp32 rounding order.
+// reference up to fp32 rounding order. The reference moves under one
+// wave-uniform branch per chunk (rarely taken), and the head's last chunk is
+// handled outside the main loop, so the loop body is a single path.
 //
 // This file is compiled with -fno-honor-nans: every input is finite, and
 // without NaNs fmaxf/fminf of MFMA results are single instructions.
@@ -207,6 +209,10 @@ __global__ __launch_bounds__(kLseThreads, 3) void lse_kernel(
         constexpr bool kTail = decltype(tail_tag)::value;
         unsigned char* ostage = out_stage + (i & 1) * kLseOutBytes;
         const int jq = c * kLseChunk + 4 * quad;  // first block of this lane
+        // fp16 pair-LSEs of each row tile, blocks (0, 1) and (2, 3) (non-tail
+        // path). Kept as whole f16x2 values: bit casts of single elements of
+        // an ext_vector read element 0 with this compiler.
+        f16x2 tile01[4], tile23[4];
 #pragma unroll
         for (int rt = 0; rt < 4; ++rt) {
             f32x4 acc[2];
@@ -247,22 +253,42 @@ __global__ __launch_bounds__(kLseThreads, 3) void lse_kernel(
 #pragma unroll
                 for (int v = 0; v < 4; ++v) den[rt] += fast_exp2(f[v] - ref[rt]);
             } else {
-                // The maximum of the four fp16 values in fp16 (exact), and
-                // f - ref straight from the fp16 halves with v_fma_mix_f32
-                // (f16 -> f32 is exact, so this is the rounded f - ref).
-                const f16x2 m2 = __builtin_elementwise_max(h01, h23);
-                const float tmax = static_cast<float>(m2[0] > m2[1] ? m2[0] : m2[1]);
-                top[rt] = fmaxf(top[rt], tmax);
-                const bool grow = tmax > ref[rt] + kLseSlack;
-                if (__any(grow)) {
-                    const float nr = grow ? tmax : ref[rt];
+                tile01[rt] = h01;
+                tile23[rt] = h23;
+            }
+        }
+        if (!kTail) {
+            // The maximum of each tile's four fp16 values in fp16 (exact).
+            // One wave-uniform branch per chunk moves the references of every
+            // row tile that needs it (rare); tiles and lanes that do not grow
+            // take nr == ref, and den * 2^0 leaves den unchanged.
+            float tmax[4];
+            bool grow_any = false;
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt) {
+                const f16x2 m2 = __builtin_elementwise_max(tile01[rt], tile23[rt]);
+                tmax[rt] = static_cast<float>(m2[0] > m2[1] ? m2[0] : m2[1]);
+                top[rt] = fmaxf(top[rt], tmax[rt]);
+                grow_any |= tmax[rt] > ref[rt] + kLseSlack;
+            }
+            if (__any(grow_any)) {
+#pragma unroll
+                for (int rt = 0; rt < 4; ++rt) {
+                    const float nr = tmax[rt] > ref[rt] + kLseSlack ? tmax[rt] : ref[rt];
                     den[rt] *= fast_exp2(ref[rt] - nr);
                     ref[rt] = nr;
                 }
-                den[rt] += fast_exp2(f16_minus<false>(packed[0], ref[rt]));
-                den[rt] += fast_exp2(f16_minus<true>(packed[0], ref[rt]));
-                den[rt] += fast_exp2(f16_minus<false>(packed[1], ref[rt]));
-                den[rt] += fast_exp2(f16_minus<true>(packed[1], ref[rt]));
+            }
+            // f - ref straight from the fp16 halves with v_fma_mix_f32
+            // (f16 -> f32 is exact, so this is the rounded f - ref).
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt) {
+                const uint32_t lo = __builtin_bit_cast(uint32_t, tile01[rt]);
+                const uint32_t hi = __builtin_bit_cast(uint32_t, tile23[rt]);
+                den[rt] += fast_exp2(f16_minus<false>(lo, ref[rt]));
+                den[rt] += fast_exp2(f16_minus<true>(lo, ref[rt]));
+                den[rt] += fast_exp2(f16_minus<false>(hi, ref[rt]));
+                den[rt] += fast_exp2(f16_minus<true>(hi, ref[rt]));
             }
         }
     };
@@ -293,27 +319,42 @@ __global__ __launch_bounds__(kLseThreads, 3) void lse_kernel(
     // its transfer may stay outstanding), read it into registers, start the
     // transfer of chunk c + 4 into the same buffer, compute chunk c into the
     // staging buffer of round i.
-    if (wave < chunks) issue_chunk(wave);
-    for (int i = 0; i < rounds; ++i) {
-        const int c = 4 * i + wave;
-        if (i > 0) store_round(i - 1);
+    auto wait_chunk = [&](int i) {
         switch (i > 0 ? n_st : 0) {
             case 2: wait_vmcnt<2>(); break;
             case 1: wait_vmcnt<1>(); break;
             default: wait_vmcnt<0>(); break;
         }
+    };
+    if (wave < chunks) issue_chunk(wave);
+    // Every round but the last: each wave's chunk c = 4i + wave <= 4 rounds - 5
+    // is complete and not the head's last (chunks > 4 (rounds - 1)), so the
+    // loop body has one path.
+    for (int i = 0; i + 1 < rounds; ++i) {
+        const int c = 4 * i + wave;
+        if (i > 0) store_round(i - 1);
+        wait_chunk(i);
+        bf16x8 a[2][4];
+        read_chunk(a);
+        if (c + 4 < chunks) issue_chunk(c + 4);
+        compute(c, i, a, std::false_type{});
+        lds_barrier();
+    }
+    if (rounds > 0) {
+        const int i = rounds - 1, c = 4 * i + wave;
+        if (i > 0) store_round(i - 1);
+        wait_chunk(i);
         if (c < chunks) {
             bf16x8 a[2][4];
             read_chunk(a);
-            if (c + 4 < chunks) issue_chunk(c + 4);
             if (c < chunks - 1)
                 compute(c, i, a, std::false_type{});
             else
                 compute(c, i, a, std::true_type{});
         }
         lds_barrier();
+        store_round(rounds - 1);
     }
-    if (rounds > 0) store_round(rounds - 1);
 
     // Rebase each lane's normaliser on its exact maximum, then merge the four
     // lanes (quads) of each centroid row and the four waves.
