@@ -106,7 +106,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=2, help="BASELINE config index (default 2)")
     ap.add_argument("--heads", type=int, default=None, help="override head count (profiling only)")
-    ap.add_argument("--cpu-sample-rows", type=int, default=8)
+    ap.add_argument("--cpu-sample-rows", type=int, default=80,
+                    help="query blocks of head 0 timed on the CPU oracle (about 10 s on the GPU box host)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy (HBM counter calibration)")
