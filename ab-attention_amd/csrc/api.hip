@@ -24,6 +24,7 @@ int launch_sip(const float* scores, const float* offsets, int64_t rows, int64_t 
                int32_t* ids, float* logw, hipStream_t stream);
 bool sip_fits(int64_t population);
 bool sip_fused_fits(int64_t population);
+void sip_force_exact_draws(int on);
 int launch_sip_fused(const void* lse, const float* pops, const float* lse_max, const float* lse_den, int64_t ld,
                      const float* offsets, int64_t rows, int64_t population, int64_t samples, int32_t* ids,
                      float* logw, hipStream_t stream);
@@ -197,9 +198,9 @@ int ab_ibcs_ordered(const void* q, const void* k, const int32_t* order, int64_t 
 
 size_t ab_ibcs_sip_workspace_bytes(int64_t batch_heads, int64_t tokens) {
     if (batch_heads <= 0 || tokens <= 0 || tokens % kKvBlock) return 0;
-    const IbcsLayout L = ibcs_layout(batch_heads, tokens);
-    // Rows too large for the fused kernel's LDS go through scores in memory.
-    return sip_fused_fits(L.fb) ? L.total : L.total + align256(size_t(L.rows) * L.fb * 4);
+    // The fused kernel samples every row in LDS (rows of up to 32,768 blocks
+    // fit), so the workspace holds only the IBCS intermediates.
+    return ibcs_layout(batch_heads, tokens).total;
 }
 
 int ab_ibcs_sip(const void* q, const void* k, const int32_t* order, int64_t batch_heads, int64_t tokens,
@@ -209,7 +210,8 @@ int ab_ibcs_sip(const void* q, const void* k, const int32_t* order, int64_t batc
     const IbcsLayout L = ibcs_layout(batch_heads, tokens);
     if (!(samples > 0 && samples < L.fb))
         return set_error(AB_ERR_INVALID, "ibcs_sip: sample count must be inside the population");
-    if (!sip_fits(L.fb)) return set_error(AB_ERR_INVALID, "ibcs_sip: population exceeds single-workgroup LDS capacity");
+    if (!sip_fused_fits(L.fb))
+        return set_error(AB_ERR_INVALID, "ibcs_sip: population exceeds the fused kernel's LDS capacity");
     if (!q || !k || !offsets || !workspace || !ids || !log_weights)
         return set_error(AB_ERR_INVALID, "ibcs_sip: null pointer");
     if (!aligned16(q) || !aligned16(k)) return set_error(AB_ERR_INVALID, "ibcs_sip: q and k must be 16-byte aligned");
@@ -229,12 +231,8 @@ int ab_ibcs_sip(const void* q, const void* k, const int32_t* order, int64_t batc
         return rc;
     if (int rc = launch_lse(ws + L.centroids, ws + L.pooled, batch_heads, tokens, ws + L.lse, lse_max, lse_den, st))
         return rc;
-    if (sip_fused_fits(L.fb))
-        return launch_sip_fused(ws + L.lse, pops, lse_max, lse_den, L.ld, offsets, L.rows, L.fb, samples, ids,
-                                log_weights, st);
-    float* scores = reinterpret_cast<float*>(ws + L.total);
-    if (int rc = launch_masses(ws + L.lse, pops, lse_max, lse_den, L.rows, L.fb, scores, st)) return rc;
-    return launch_sip(scores, offsets, L.rows, L.fb, samples, ids, log_weights, st);
+    return launch_sip_fused(ws + L.lse, pops, lse_max, lse_den, L.ld, offsets, L.rows, L.fb, samples, ids,
+                            log_weights, st);
 }
 
 int ab_sip(const float* scores, const float* offsets, int64_t rows, int64_t population, int64_t samples,
@@ -344,6 +342,11 @@ int ab_merge_states(const void* o_a, const float* lse_a, const void* o_b, const 
         return set_error(AB_ERR_INVALID, "merge_states: states must be 16-byte aligned");
     if (count > (int64_t(1) << 35)) return set_error(AB_ERR_INVALID, "merge_states: too many rows");
     return launch_merge(o_a, lse_a, o_b, lse_b, count, out, lse_out, static_cast<hipStream_t>(stream));
+}
+
+int ab_testing_force_exact_draws(int on) {
+    sip_force_exact_draws(on);
+    return AB_OK;
 }
 
 }  // extern "C"

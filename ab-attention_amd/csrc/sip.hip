@@ -113,6 +113,7 @@ struct SipShared {
     double scale;
     int added, pass, last;
     int wave_count[kSipThreads / 64];
+    int exact;  // coarse prefixes: the row needs the reference's probe sequence
 };
 
 // Thread-strided partial (sum, max) over the non-certain masses: thread t
@@ -157,14 +158,238 @@ __device__ __forceinline__ void strided_partials(const R& rv, int pop, double& s
     mx = static_cast<double>(__uint_as_float(top));
 }
 
+// Bucket prefixes and draws from coarse prefixes (the tail of sip_row for
+// kCoarse). The reference's bucket prefixes (sip.cu:131-142) are one fp64
+// chain per chunk of 4*cb blocks: prefix[b] = R (residual count) if bucket b
+// starts past the last non-certain block, else the chain E[c] + the chunk's
+// masses before bucket b, added in order. Only three prefixes per chunk are
+// kept: its first (E[c] = sh.part[c] after the scan), its middle (bucket
+// c*cb + ceil(cb/2)) and its last; any other is the same chain continued from
+// the nearest kept one, which gives the same bits.
+// A draw with threshold th (sip.cu:144-166) needs the bucket the reference's
+// binary search returns. Chains only grow, so the prefix array can fall only
+// where a chunk's last prefix exceeds the next chunk's first (rounding of the
+// scan against the chain) or where it drops to R (no threshold reaches R).
+// If no threshold lies in such a drop at a chunk boundary, exactly one bucket
+// b has prefix[b] <= th < prefix[b + 1], and the binary search returns it
+// whatever its probes: the draw then finds it with a binary search over the
+// kept prefixes and a walk of at most ceil(cb/2) buckets. Each chunk checks
+// its boundary; a row where some threshold lands in a drop (sh.exact) makes
+// the reference's probes instead, each prefix rebuilt from the kept ones.
+template <int kWorkers, class R, class StageNext>
+__device__ __forceinline__ void coarse_draws(R& rv, double* coarse, SipShared& sh, float offset_u,
+                                             int32_t* __restrict__ out_ids, float* __restrict__ out_w, int pop,
+                                             int residuals, int certainty, int last, double scale, int chunk,
+                                             StageNext stage_next) {
+    const int t = threadIdx.x;
+    const int buckets = (pop + kBucket - 1) / kBucket;
+    const int cb = chunk / kBucket;   // buckets per chunk
+    const int half = (cb + 1) / 2;    // chunk-relative middle bucket
+    const double rd = static_cast<double>(residuals);
+    const double offset = static_cast<double>(offset_u);
+    double* mid = coarse;                // [256] prefix at each chunk's middle bucket
+    double* tail = coarse + kSipThreads;  // [256] prefix at each chunk's last bucket
+    auto chunk_end = [&](int c) { return min((c + 1) * cb, buckets); };
+    auto mid_bucket = [&](int c) { return min(c * cb + half, chunk_end(c)); };
+    // prefix[c * cb]: the chunk's scan value, or R past the last residual
+    // (and for the terminal bucket).
+    auto first_prefix = [&](int c) -> double {
+        if (c >= kSipThreads || c * cb >= buckets || kBucket * (c * cb) > last) return rd;
+        return sh.part[c];
+    };
+    // The chain over the 4 blocks of bucket b (sip.cu:137-140).
+    auto add_bucket = [&](int b, double cum) -> double {
+        float r[8];
+        rv.raw8(b * kBucket, r);
+#pragma unroll
+        for (int e = 0; e < kBucket; ++e) {
+            const int i = b * kBucket + e;
+            const bool ok = i < pop && !rv.certain_of(i, r[e]);
+            const double m = static_cast<double>(R::x_of(r[e])) * scale;
+            cum = cum + (ok ? m : 0.0);
+        }
+        return cum;
+    };
+
+    // Kept prefixes: the same chain walk as the reference's prefix pass.
+    if (t < kSipThreads) {
+        const int begin = t * chunk, end = min(begin + chunk, pop);
+        double vmid = rd, vlast = rd;
+        if (begin < pop) {
+            double cumulative = sh.part[t];
+            int i0 = begin;
+            if (certainty == 0) {
+                for (; i0 + 8 <= end; i0 += 8) {
+                    float r[8];
+                    rv.raw8(i0, r);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        if (e % kBucket == 0) {
+                            if ((i0 + e) / kBucket - t * cb == half) vmid = cumulative;
+                            vlast = cumulative;
+                        }
+                        cumulative = cumulative + static_cast<double>(R::x_of(r[e])) * scale;
+                    }
+                }
+            }
+            for (; i0 < end; i0 += 8) {
+                float r[8];
+                rv.raw8(i0, r);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int i = i0 + e;
+                    if (e % kBucket == 0 && i < end) {
+                        const double v = i > last ? rd : cumulative;
+                        if (i / kBucket - t * cb == half) vmid = v;
+                        vlast = v;
+                    }
+                    const bool ok = i < end && !rv.certain_of(i, r[e]);
+                    const double m = static_cast<double>(R::x_of(r[e])) * scale;
+                    cumulative = cumulative + (ok ? m : 0.0);
+                }
+            }
+            // No middle bucket inside the chunk: the kept value is the next
+            // chunk's first prefix.
+            if (mid_bucket(t) == chunk_end(t)) vmid = first_prefix(t + 1);
+            // A drop at the boundary with the next chunk: does some threshold
+            // offset + s (0 <= s < residuals, exact in fp64) lie in it?
+            const double next = first_prefix(t + 1);
+            if (vlast > next) {
+                double s = ceil(next - offset);
+                while (s > 0.0 && offset + (s - 1.0) >= next) s -= 1.0;
+                while (offset + s < next) s += 1.0;
+                s = fmax(s, 0.0);
+                if (s < rd && offset + s < vlast && offset + s >= next) atomicOr(&sh.exact, 1);
+            }
+        }
+        mid[t] = vmid;
+        tail[t] = vlast;
+    }
+    lds_barrier();
+
+    // Kept prefixes in bucket order: entry k is chunk k/2's first (k even) or
+    // middle (k odd) bucket.
+    auto kept_value = [&](int k) -> double { return (k & 1) ? mid[k >> 1] : first_prefix(k >> 1); };
+    auto kept_bucket = [&](int k) -> int {
+        return k >= 2 * kSipThreads ? buckets : ((k & 1) ? mid_bucket(k >> 1) : min((k >> 1) * cb, buckets));
+    };
+    // prefix[b] rebuilt from the nearest kept prefix at or before it.
+    auto prefix_at = [&](int b) -> double {
+        if (b >= buckets || kBucket * b > last) return rd;
+        const int c = b / cb, mb = mid_bucket(c);
+        int b0 = c * cb;
+        double cum = sh.part[c];
+        if (b >= mb && mb < chunk_end(c)) {
+            b0 = mb;
+            cum = mid[c];
+        }
+        for (int bb = b0; bb < b; ++bb) cum = add_bucket(bb, cum);
+        return cum;
+    };
+    const bool exact = sh.exact != 0;
+    const int per_round = kWorkers * kDraws;
+    const int rounds = (residuals + per_round - 1) / per_round;
+    for (int round = 0; round < rounds; ++round) {
+        const int slot0 = t + round * per_round;
+        double threshold[kDraws];
+        int bucket[kDraws];
+        double base[kDraws];
+#pragma unroll
+        for (int d = 0; d < kDraws; ++d) threshold[d] = offset + static_cast<double>(slot0 + d * kWorkers);
+        if (!exact) {
+            // Binary search over the kept prefixes (2 per chunk), the draws in
+            // lockstep, then each walks its segment to the crossing bucket.
+            int lower[kDraws], upper[kDraws];
+#pragma unroll
+            for (int d = 0; d < kDraws; ++d) {
+                lower[d] = 0;
+                upper[d] = slot0 + d * kWorkers < residuals ? 2 * kSipThreads - 1 : 0;
+            }
+            bool busy = true;
+            while (busy) {
+                busy = false;
+#pragma unroll
+                for (int d = 0; d < kDraws; ++d)
+                    if (lower[d] < upper[d]) {
+                        const int middle = (lower[d] + upper[d] + 1) / 2;
+                        if (kept_value(middle) <= threshold[d]) lower[d] = middle;
+                        else upper[d] = middle - 1;
+                        busy = true;
+                    }
+            }
+#pragma unroll
+            for (int d = 0; d < kDraws; ++d) {
+                int b = kept_bucket(lower[d]);
+                double cum = kept_value(lower[d]);
+                const int bend = kept_bucket(lower[d] + 1);
+                while (b + 1 < bend) {
+                    const double nxt = add_bucket(b, cum);
+                    if ((kBucket * (b + 1) > last ? rd : nxt) > threshold[d]) break;
+                    cum = nxt;
+                    ++b;
+                }
+                bucket[d] = min(b, buckets - 1);
+                base[d] = cum;
+            }
+        } else {
+#pragma unroll
+            for (int d = 0; d < kDraws; ++d) {
+                int lower = 0, upper = slot0 + d * kWorkers < residuals ? buckets : 0;
+                while (lower < upper) {
+                    const int middle = (lower + upper + 1) / 2;
+                    if (prefix_at(middle) <= threshold[d]) lower = middle;
+                    else upper = middle - 1;
+                }
+                bucket[d] = min(lower, buckets - 1);
+                base[d] = prefix_at(bucket[d]);
+            }
+        }
+        int selected[kDraws];
+        float weight[kDraws];
+#pragma unroll
+        for (int d = 0; d < kDraws; ++d) {
+            double mass = base[d];
+            int sel = last;
+            float r[8];
+            rv.raw8(bucket[d] * kBucket, r);
+#pragma unroll
+            for (int e = 0; e < kBucket; ++e) {
+                const int i = bucket[d] * kBucket + e;
+                if (i >= pop || rv.certain_of(i, r[e])) continue;
+                sel = i;
+                mass = fma(static_cast<double>(R::x_of(r[e])), scale, mass);
+                if (mass > threshold[d]) break;
+            }
+            selected[d] = sel;
+            weight[d] = static_cast<float>(-log2(rv.weight_mass(sel) * scale));
+        }
+        if (round + 1 == rounds) {
+            lds_barrier();
+            stage_next();
+        }
+#pragma unroll
+        for (int d = 0; d < kDraws; ++d) {
+            const int slot = slot0 + d * kWorkers;
+            if (slot < residuals) {
+                out_ids[certainty + slot] = selected[d];
+                out_w[certainty + slot] = weight[d];
+            }
+        }
+    }
+    if (rounds == 0) {
+        lds_barrier();
+        stage_next();
+    }
+}
+
 // Everything after the first pass's thread partials are known: certainty
 // iteration, certain ids, chunk scan, bucket prefixes and the draws. Inlined:
 // a called function starts by waiting for every outstanding memory access,
 // which would stall on the next row's prefetch.
-template <class R, class StageNext>
+template <int kWorkers, bool kCoarse, class R, class StageNext>
 __device__ __forceinline__ void sip_row(R& rv, double sum, double mx, double* prefix, SipShared& sh, float offset_u,
                                         int32_t* __restrict__ out_ids, float* __restrict__ out_w, int pop,
-                                        int samples, StageNext stage_next) {
+                                        int samples, StageNext stage_next, int exact_init = 0) {
     const int t = threadIdx.x;
     const bool logical = t < kSipThreads;
     const int buckets = (pop + kBucket - 1) / kBucket;
@@ -203,7 +428,7 @@ __device__ __forceinline__ void sip_row(R& rv, double sum, double mx, double* pr
         scale = sh.scale;
         if (sh.pass) {
             int count = 0;
-            for (int i = t; i < pop; i += kSipWorkers)
+            for (int i = t; i < pop; i += kWorkers)
                 if (!rv.certain(i) && static_cast<double>(rv.x(i)) * scale >= 1.0) {
                     rv.mark(i);
                     ++count;
@@ -224,7 +449,7 @@ __device__ __forceinline__ void sip_row(R& rv, double sum, double mx, double* pr
         if (t == 0) sh.last = -1;
         lds_barrier();
         int mine = -1;
-        for (int i = t; i < pop; i += kSipWorkers)
+        for (int i = t; i < pop; i += kWorkers)
             if (!rv.certain(i)) mine = i;
         if (mine >= 0) atomicMax(&sh.last, mine);
         lds_barrier();
@@ -293,6 +518,7 @@ __device__ __forceinline__ void sip_row(R& rv, double sum, double mx, double* pr
         }
         sh.part[t] = chunk_mass;
     }
+    if (kCoarse && t == 0) sh.exact = exact_init;
     lds_barrier();
     if (t < 32) {
         double seg = sh.part[8 * t];
@@ -316,8 +542,14 @@ __device__ __forceinline__ void sip_row(R& rv, double sum, double mx, double* pr
     }
     lds_barrier();
 
-    // Bucket prefixes (sip.cu:131-142).
     const int residuals = samples - certainty;
+    if constexpr (kCoarse) {
+        coarse_draws<kWorkers>(rv, prefix, sh, offset_u, out_ids, out_w, pop, residuals, certainty, last, scale,
+                               chunk, stage_next);
+        return;
+    }
+
+    // Bucket prefixes (sip.cu:131-142).
     if (t == 0) prefix[buckets] = static_cast<double>(residuals);
     if (logical) {
         double cumulative = sh.part[t];
@@ -358,7 +590,7 @@ __device__ __forceinline__ void sip_row(R& rv, double sum, double mx, double* pr
     // every thread is done reading this one), so that the next row's prefetch
     // never waits behind these stores.
     const double offset = static_cast<double>(offset_u);
-    const int per_round = kSipWorkers * kDraws;
+    const int per_round = kWorkers * kDraws;
     const int rounds = (residuals + per_round - 1) / per_round;
     for (int round = 0; round < rounds; ++round) {
         const int slot0 = t + round * per_round;
@@ -366,7 +598,7 @@ __device__ __forceinline__ void sip_row(R& rv, double sum, double mx, double* pr
         double threshold[kDraws];
 #pragma unroll
         for (int d = 0; d < kDraws; ++d) {
-            const int slot = slot0 + d * kSipWorkers;
+            const int slot = slot0 + d * kWorkers;
             threshold[d] = offset + static_cast<double>(slot);
             lower[d] = 0;
             upper[d] = slot < residuals ? buckets : 0;
@@ -409,7 +641,7 @@ __device__ __forceinline__ void sip_row(R& rv, double sum, double mx, double* pr
         }
 #pragma unroll
         for (int d = 0; d < kDraws; ++d) {
-            const int slot = slot0 + d * kSipWorkers;
+            const int slot = slot0 + d * kWorkers;
             if (slot < residuals) {
                 out_ids[certainty + slot] = selected[d];
                 out_w[certainty + slot] = weight[d];
@@ -468,31 +700,44 @@ __global__ __launch_bounds__(kSipWorkers) void sip_lds_kernel(
         LdsRow rv{values};
         double sum = 0.0, mx = 0.0;
         if (t < kSipThreads) strided_partials<true>(rv, pop, sum, mx);
-        sip_row(rv, sum, mx, prefix, sh, offsets[row], ids + row * int64_t(samples),
-                logw + row * int64_t(samples), pop, samples, [&] {
-                    if (following < rows) stage();
-                });
+        sip_row<kSipWorkers, false>(rv, sum, mx, prefix, sh, offsets[row], ids + row * int64_t(samples),
+                                    logw + row * int64_t(samples), pop, samples, [&] {
+                                        if (following < rows) stage();
+                                    });
     }
 }
 
-// Fused masses + SIP for rows that fit in LDS: each persistent workgroup
-// computes its row's masses from the fp16 pair-LSEs [8, ld] straight into
-// LDS (RowMasses: the arithmetic of masses_kernel, so the same bits as the
-// scores that kernel writes), then samples the row as sip_lds_kernel does.
-// The scores never go to global memory. A row's pair-LSEs are loaded two
-// groups of 8 blocks per thread at a time (16 loads in flight).
+// Fused masses + SIP for rows whose masses fit in LDS: each persistent
+// workgroup computes its row's masses from the fp16 pair-LSEs [8, ld]
+// straight into LDS (RowMasses: the arithmetic of masses_kernel, so the same
+// bits as the scores that kernel writes), then samples the row as
+// sip_lds_kernel does. The scores never go to global memory. A row's
+// pair-LSEs are loaded two groups of 8 blocks per thread at a time (16 loads
+// in flight).
+// kCoarse = false: LDS holds the fp64 bucket prefixes and the masses (c2:
+//   113 KB, one workgroup per CU).
+// kCoarse = true, for rows whose full prefix array does not fit (c3's 29,700
+//   blocks): LDS holds the masses and two kept prefixes per chunk
+//   (coarse_draws).
+// Two 512-thread workgroups per CU with kept prefixes were tried at c2
+// (81.9 KB each): 4.89 ms against 4.14 ms for this layout.
+__host__ __device__ constexpr size_t sip_fused_coarse_offset(int64_t population) {
+    return (size_t(population + 8) * 4 + 15) / 16 * 16;
+}
+
+template <bool kCoarse>
 __global__ __launch_bounds__(kSipWorkers) void sip_fused_kernel(
     const _Float16* __restrict__ lse, const float* __restrict__ pops, const float* __restrict__ lse_max,
     const float* __restrict__ lse_den, int64_t ld, const float* __restrict__ offsets, int32_t* __restrict__ ids,
-    float* __restrict__ logw, int population, int samples, int64_t rows) {
+    float* __restrict__ logw, int population, int samples, int64_t rows, int force_exact) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ SipShared sh;
     const int t = threadIdx.x;
     const int pop = population;
     const int buckets = (pop + kBucket - 1) / kBucket;
     const int groups = (pop + 7) / 8;
-    double* prefix = reinterpret_cast<double*>(smem);
-    float* values = reinterpret_cast<float*>(smem + sip_values_offset(buckets));
+    double* prefix = reinterpret_cast<double*>(kCoarse ? smem + sip_fused_coarse_offset(pop) : smem);
+    float* values = reinterpret_cast<float*>(kCoarse ? smem : smem + sip_values_offset(buckets));
     for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
         // The previous row's last reads of values[] finished before the
         // barrier ahead of its stores, so the row can be written over.
@@ -523,8 +768,8 @@ __global__ __launch_bounds__(kSipWorkers) void sip_fused_kernel(
         LdsRow rv{values};
         double sum = 0.0, mx = 0.0;
         if (t < kSipThreads) strided_partials<true>(rv, pop, sum, mx);
-        sip_row(rv, sum, mx, prefix, sh, offsets[row], ids + row * int64_t(samples), logw + row * int64_t(samples),
-                pop, samples, [] {});
+        sip_row<kSipWorkers, kCoarse>(rv, sum, mx, prefix, sh, offsets[row], ids + row * int64_t(samples),
+                                      logw + row * int64_t(samples), pop, samples, [] {}, force_exact);
     }
 }
 
@@ -543,8 +788,8 @@ __global__ __launch_bounds__(kSipWorkers) void sip_global_kernel(
     lds_barrier();
     double sum = 0.0, mx = 0.0;
     if (t < kSipThreads) strided_partials<true>(rv, pop, sum, mx);
-    sip_row(rv, sum, mx, prefix, sh, offsets[row], ids + row * int64_t(samples), logw + row * int64_t(samples),
-            pop, samples, [] {});
+    sip_row<kSipWorkers, false>(rv, sum, mx, prefix, sh, offsets[row], ids + row * int64_t(samples),
+                                logw + row * int64_t(samples), pop, samples, [] {});
 }
 
 template <int kPer>
@@ -576,16 +821,33 @@ size_t sip_lds_bytes(int64_t population, bool lds_values) {
 
 bool sip_fits(int64_t population) { return sip_lds_bytes(population, false) + kSipStaticLds <= kLdsLimit; }
 
-bool sip_fused_fits(int64_t population) { return sip_lds_bytes(population, true) + kSipStaticLds <= kLdsLimit; }
+// The fused kernel's LDS: the bucket prefixes and the masses, or (rows too
+// large for that) the masses and two kept prefixes per chunk.
+size_t sip_fused_lds_bytes(int64_t population, bool coarse) {
+    return coarse ? sip_fused_coarse_offset(population) + size_t(2 * kSipThreads) * sizeof(double)
+                  : sip_lds_bytes(population, true);
+}
 
-int launch_sip_fused(const void* lse, const float* pops, const float* lse_max, const float* lse_den, int64_t ld,
-                     const float* offsets, int64_t rows, int64_t population, int64_t samples, int32_t* ids,
-                     float* logw, hipStream_t stream) {
-    if (!sip_fused_fits(population))
-        return set_error(1, "sip: population %lld does not fit the fused kernel's LDS", (long long)population);
-    if (rows == 0) return 0;
-    const size_t bytes = sip_lds_bytes(population, true);
-    const void* fn = reinterpret_cast<const void*>(sip_fused_kernel);
+bool sip_fused_fits(int64_t population) {
+    return sip_fused_lds_bytes(population, true) + kSipStaticLds <= kLdsLimit;
+}
+static_assert(sip_fused_coarse_offset(kMaxKvBlocks) + 2 * kSipThreads * sizeof(double) + kSipStaticLds <= kLdsLimit,
+              "every row the API accepts fits the fused kernel's LDS");
+
+// Testing hook: every row sampled with kept prefixes takes the reference's
+// probe sequence (the path otherwise used only when a threshold lands in a
+// rounding drop of the prefix array, which the tests cannot construct).
+static int g_force_exact = 0;
+void sip_force_exact_draws(int on) { g_force_exact = on != 0; }
+
+namespace {
+
+template <bool kCoarse>
+int launch_fused(const _Float16* lse, const float* pops, const float* lse_max, const float* lse_den, int64_t ld,
+                 const float* offsets, int64_t rows, int pop, int samples, int32_t* ids, float* logw,
+                 hipStream_t stream) {
+    const size_t bytes = sip_fused_lds_bytes(pop, kCoarse);
+    const void* fn = reinterpret_cast<const void*>(sip_fused_kernel<kCoarse>);
     (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
     int device = 0, cus = 0, per_cu = 0;
     (void)hipGetDevice(&device);
@@ -593,10 +855,25 @@ int launch_sip_fused(const void* lse, const float* pops, const float* lse_max, c
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kSipWorkers, bytes) != hipSuccess || per_cu < 1)
         per_cu = 1;
     const int64_t grid = std::min<int64_t>(rows, int64_t(std::max(cus, 1)) * per_cu);
-    hipLaunchKernelGGL(sip_fused_kernel, dim3(static_cast<unsigned>(grid)), dim3(kSipWorkers), bytes, stream,
-                       static_cast<const _Float16*>(lse), pops, lse_max, lse_den, ld, offsets, ids, logw,
-                       static_cast<int>(population), static_cast<int>(samples), rows);
+    hipLaunchKernelGGL(sip_fused_kernel<kCoarse>, dim3(static_cast<unsigned>(grid)), dim3(kSipWorkers), bytes,
+                       stream, lse, pops, lse_max, lse_den, ld, offsets, ids, logw, pop, samples, rows,
+                       g_force_exact);
     return check_launch("sip_fused_kernel");
+}
+
+}  // namespace
+
+int launch_sip_fused(const void* lse, const float* pops, const float* lse_max, const float* lse_den, int64_t ld,
+                     const float* offsets, int64_t rows, int64_t population, int64_t samples, int32_t* ids,
+                     float* logw, hipStream_t stream) {
+    if (!sip_fused_fits(population))
+        return set_error(1, "sip: population %lld does not fit the fused kernel's LDS", (long long)population);
+    if (rows == 0) return 0;
+    const _Float16* h = static_cast<const _Float16*>(lse);
+    const int pop = static_cast<int>(population), s = static_cast<int>(samples);
+    if (sip_fused_lds_bytes(population, false) + kSipStaticLds <= kLdsLimit)
+        return launch_fused<false>(h, pops, lse_max, lse_den, ld, offsets, rows, pop, s, ids, logw, stream);
+    return launch_fused<true>(h, pops, lse_max, lse_den, ld, offsets, rows, pop, s, ids, logw, stream);
 }
 
 int launch_sip(const float* scores, const float* offsets, int64_t rows, int64_t population, int64_t samples,

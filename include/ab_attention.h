@@ -79,14 +79,22 @@ int ab_sip(const float *scores, const float *offsets, int64_t rows, int64_t popu
  * _C.sip) in one call: q, k bf16 [batch_heads, tokens, 128] (tokens read
  * through `order` when it is not NULL, as ab_ibcs_ordered), offsets f32
  * [rows] -> ids int32 / log_weights f32 [rows, samples], the same bits as
- * ab_ibcs followed by ab_sip. Rows whose masses fit in LDS are scored and
- * sampled by one kernel that computes each row's masses straight into LDS;
- * larger rows go through scores in the workspace. `workspace` is
- * ab_ibcs_sip_workspace_bytes() bytes, 256-byte aligned. */
+ * ab_ibcs followed by ab_sip. Every row is scored and sampled by one kernel
+ * that computes its masses straight into LDS (rows over ~26,000 blocks keep
+ * two fp64 prefixes per chunk instead of all bucket prefixes); the scores are
+ * never written. `workspace` is ab_ibcs_sip_workspace_bytes() bytes, 256-byte
+ * aligned. */
 size_t ab_ibcs_sip_workspace_bytes(int64_t batch_heads, int64_t tokens);
 int ab_ibcs_sip(const void *q, const void *k, const int32_t *order, int64_t batch_heads, int64_t tokens,
                 const float *offsets, int64_t samples, void *workspace, size_t workspace_bytes, int32_t *ids,
                 float *log_weights, void *stream);
+
+/* Testing hook; no counterpart in the reference. With `on` nonzero, every row
+ * that ab_ibcs_sip samples with kept prefixes takes the reference's
+ * binary-search probes (each prefix rebuilt from the kept ones), the path
+ * otherwise taken only when a threshold lands in a rounding drop of the
+ * prefix array. The bits are the same either way. Process-wide; returns 0. */
+int ab_testing_force_exact_draws(int on);
 
 /* ---- Weighted paged prefill ------------------------------------------------
  * Replaces the FlashInfer FA3 run with the ABSipAttention variant

@@ -5,7 +5,7 @@ each row's masses with the masses kernel's arithmetic straight into LDS."""
 import pytest
 import torch
 
-from ab_attention import _C, build_plan
+from ab_attention import _C, _lib, build_plan
 from ab_attention.synthetic import CONFIGS, make_qkv
 
 pytestmark = pytest.mark.gpu
@@ -56,14 +56,31 @@ def test_fused_plan_ordered():
     _assert_same(*_both(q, k, 256, order=order, seed=1))
 
 
-def test_fused_plan_large_rows_fallback():
-    """27,000 blocks per row do not fit the fused kernel's LDS: the masses go
-    through memory (masses kernel, then the global-memory SIP kernel)."""
-    print("fused plan fallback n=108000", flush=True)
+@pytest.mark.parametrize("n", [108000, 131072])
+def test_fused_plan_large_rows(n):
+    """27,000 and 32,768 (the most the API accepts) blocks per row: the full
+    fp64 prefix array does not fit in LDS beside the masses, so the fused kernel
+    keeps two prefixes per chunk."""
+    print(f"fused plan large rows n={n}", flush=True)
     torch.manual_seed(8)
-    n = 108000
     q, k = (torch.randn(1, 1, n, 128).to(torch.bfloat16).cuda() for _ in range(2))
     _assert_same(*_both(q, k, 2048, seed=2))
+
+
+def test_fused_plan_exact_probe_path():
+    """With kept prefixes, a row whose thresholds could land in a rounding drop
+    of the prefix array makes the reference's probes instead of the two-level
+    search; forcing that path for every row gives the same bits."""
+    print("fused plan forced reference probes n=108000", flush=True)
+    torch.manual_seed(9)
+    n = 108000
+    q, k = (torch.randn(1, 2, n, 128).to(torch.bfloat16).cuda() for _ in range(2))
+    lib = _lib.load()
+    lib.ab_testing_force_exact_draws(1)
+    try:
+        _assert_same(*_both(q, k, 2048, seed=4))
+    finally:
+        lib.ab_testing_force_exact_draws(0)
 
 
 def test_build_plan_uses_fused_path():
