@@ -99,7 +99,7 @@ def ibcs_sip(q: torch.Tensor, k: torch.Tensor, offsets: torch.Tensor, ids: torch
     """``sip(ibcs(q, k), offsets, ids, logs)`` in one native call (ab_ibcs_sip).
 
     The same ids and weights bit for bit, without materialising the scores:
-    rows whose masses fit in LDS are scored and sampled by one kernel. With
+    one kernel computes each row's masses into LDS and samples the row. With
     ``order`` (int32 [tokens]) the tokens are read through that permutation,
     as ``ibcs_ordered``. This is build_plan's per-chunk work
     (reference: attention.py:65-75).

@@ -30,6 +30,9 @@
 //   - sip_global_kernel (larger rows): one row per workgroup, the row is
 //     re-read from L2 by each pass, LDS holds the prefixes and a certainty
 //     bitmask.
+// The fused plan (sip_fused_kernel, below) computes each row's masses into
+// LDS from the pair-LSEs and samples it there; rows too large for the full
+// prefix array keep two prefixes per chunk (coarse_draws).
 #include <algorithm>
 
 #include "common.hpp"
