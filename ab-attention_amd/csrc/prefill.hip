@@ -317,6 +317,11 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
 #pragma unroll
         for (int r = 0; r < 16; ++r) sn[r] = 0.f;
         __builtin_amdgcn_sched_barrier(0);
+        // Phase A runs at wave priority 1, phase B at 0: when the SIMD's two
+        // waves compete for issue, the one computing the next tile's logits
+        // goes first (0.9 % faster at c2 than equal priorities; priority 3,
+        // or raising it from the barrier on, was slower).
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             sn = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ka[j]), bq[j], sn, 0, 0, 0);
@@ -337,6 +342,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
         for (int g = 0; g < 4; ++g) wm[g] = wn[g] - m_run;
         mx = -INFINITY;
         __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(0);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int ks = j >> 2;
