@@ -563,16 +563,11 @@ int launch_prefill(const void* q, const void* k, const void* v, bool v_kv4t, int
         return set_error(1, "prefill: one head of K/V must be under 4 GiB");
     const float scale_log2 = static_cast<float>(1.4426950408889634 / 11.313708498984761);  // log2(e)/sqrt(128)
     const int64_t per_xcd = (qb + 7) / 8;
-    static bool attr_set = false;
-    if (!attr_set) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_kernel<false>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_kernel<true>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
-        attr_set = true;
-    }
     if (rows == 0) return 0;
     auto kernel = v_kv4t ? prefill_kernel<true> : prefill_kernel<false>;
+    // The attribute is per device: set it on every launch (a host-side call).
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              kLdsBytes);
     hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(per_xcd * 8 * bh)), dim3(kPfThreads), kLdsBytes,
                        stream, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                        static_cast<const uint16_t*>(v), ids, logw, static_cast<uint16_t*>(out), lse, n, n_kv, qb, rows,
