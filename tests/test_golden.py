@@ -77,3 +77,35 @@ def test_gpu_matches_fixture(native, fx):
     assert np.abs(got - fx["out"]).max() <= 2e-2
     assert np.linalg.norm(got - fx["out"]) / np.linalg.norm(fx["out"]) <= 1e-2
     assert np.abs(lse.cpu().numpy().reshape(1, n) - fx["out_lse"]).max() <= 1e-3
+
+
+@pytest.mark.gpu
+def test_gpu_end_to_end_plan(oracle_mod, fx):
+    """Parity protocol (4): the GPU's own plan (fused IBCS + SIP on the
+    fixture's uniforms) into the GPU prefill, against the fp64 oracle prefill
+    given that same plan (bf16 bar); the share of plan ids equal to the
+    oracle's own plan is reported (IBCS masses agree to ~1e-6, so it is
+    nearly 1, but it is not a parity gate)."""
+    from ab_attention import _C
+    from ab_attention.flashinfer_backend import paged_attention
+
+    n = fx["q"].shape[1]
+    rows, _ = fx["scores"].shape
+    pages = int(fx["sample_pages"])
+    q, k, v = (_dev(fx[t]).reshape(1, 1, n, 128) for t in ("q", "k", "v"))
+    ids = torch.empty((rows, pages * 32), dtype=torch.int32, device="cuda")
+    logw = torch.empty((rows, pages * 32), dtype=torch.float32, device="cuda")
+    _C.ibcs_sip(q, k, torch.from_numpy(fx["offsets"]).cuda(), ids, logw)
+    out, lse = paged_attention(q, k, v, ids.reshape(rows, pages, 32), logw.reshape(rows, pages, 32),
+                               return_lse=True)
+    torch.cuda.synchronize()
+    ids_g, logw_g = ids.cpu().numpy(), logw.cpu().numpy()
+    f32 = lambda b: oracle_mod.bits_to_f32(b).reshape(1, n, 128)
+    want, want_lse = oracle_mod.prefill(f32(fx["q"]), f32(fx["k"]), f32(fx["v"]), ids_g, logw_g)
+    got = out.float().cpu().numpy().reshape(1, n, 128)
+    assert np.abs(got - want).max() <= 2e-2
+    assert np.linalg.norm(got - want) / np.linalg.norm(want) <= 1e-2
+    assert np.abs(lse.cpu().numpy().reshape(1, n) - want_lse).max() <= 1e-3
+    match = float(np.mean(ids_g == fx["ids"]))
+    print(f"end-to-end c0: plan ids equal to the oracle's own plan: {match:.4f}", flush=True)
+    assert match > 0.5
