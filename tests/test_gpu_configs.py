@@ -113,3 +113,33 @@ def test_c4_cube_layout_head(oracle_mod):
     _check_rows(_f32(out_cube).reshape(n, 128), ref[0], keep, n)
     # raster order restored: token i of `out` is cube position inverse[i]
     assert torch.equal(out.index_select(2, order), out_cube)
+
+
+def test_c1_plan_against_oracle_plan(oracle_mod):
+    """Parity protocol (4) on a full-length c1 head (32,760 tokens, 2,048 of
+    8,190 blocks per row): the share of the GPU plan's ids equal to the
+    oracle's own plan (oracle IBCS and SIP on the same uniforms) is reported,
+    not gated; the output over the GPU plan is checked on four rows."""
+    from ab_attention import SamplePlan
+
+    cfg = CONFIGS[1]
+    print("c1 head 0: GPU plan against the oracle's plan", flush=True)
+    q, k, v = (t[:1].contiguous() for t in make_qkv(cfg, heads=[0], device="cuda", dtype=torch.bfloat16))
+    n = q.shape[2]
+    rows, pages = -(-n // 128), cfg.sample_pages
+    samples = pages * 32
+    offsets = torch.rand(rows, generator=torch.Generator().manual_seed(5))
+    ids = torch.empty((rows, samples), dtype=torch.int32, device="cuda")
+    w = torch.empty((rows, samples), dtype=torch.float32, device="cuda")
+    _C.ibcs_sip(q, k, offsets.cuda(), ids, w)
+    out = apply_plan(q, k, v, SamplePlan(ids.reshape(rows, pages, 32), w.reshape(rows, pages, 32)))
+    torch.cuda.synchronize()
+    bits = lambda t: t.cpu().view(torch.int16).numpy().view(np.uint16).reshape(1, n, 128)
+    ids_o, _ = oracle_mod.sip(oracle_mod.ibcs(bits(q), bits(k), 1, n), offsets.numpy(), samples)
+    ids_g, w_g = ids.cpu().numpy(), w.cpu().numpy()
+    match = float(np.mean(ids_g == ids_o))
+    print(f"c1 head 0: plan ids equal to the oracle's own plan: {match:.4f}", flush=True)
+    assert match > 0.5
+    keep = np.array([0, 1, rows // 2, rows - 1])
+    ref, _ = oracle_mod.prefill(*(_f32(t).reshape(1, n, 128) for t in (q, k, v)), ids_g, w_g, rows=keep)
+    _check_rows(_f32(out).reshape(n, 128), ref[0], keep, n)
