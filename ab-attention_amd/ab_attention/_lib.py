@@ -37,14 +37,13 @@ SIGNATURES = {
     "ab_ibcs_ordered": (ctypes.c_int, [_P, _P, _P, _I64, _I64, _P, _SZ, _P, _P]),
     "ab_remap_ids": (ctypes.c_int, [_P, _I64, _P, _I64, _P, _P]),
     "ab_paged_prefill_ordered": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _P, _P, _I64, _P, _P, _P]),
-    "ab_kv4_transpose": (ctypes.c_int, [_P, _I64, _I64, _P, _P]),
     "ab_ibcs_sip_workspace_bytes": (_SZ, [_I64, _I64]),
     "ab_ibcs_sip": (ctypes.c_int, [_P, _P, _P, _I64, _I64, _P, _I64, _P, _SZ, _P, _P, _P]),
-    "ab_testing_force_exact_draws": (ctypes.c_int, [ctypes.c_int]),
-    "ab_paged_prefill_kv4t": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _P, _P, _P]),
+    "ab_ibcs_sip_exact_draws": (ctypes.c_int, [_P, _P, _P, _I64, _I64, _P, _I64, _P, _SZ, _P, _P, _P]),
+    "ab_dense_prefill": (ctypes.c_int, [_P, _P, _P, _I64, _I64, _I64, _P, _P, _P]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 _lib = None
 
 

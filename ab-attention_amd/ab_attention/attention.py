@@ -21,15 +21,15 @@ _LSE_BUDGET_BYTES = 16 * 1024 * 1024 * 1024
 
 
 class SamplePlan(NamedTuple):
-    """SIP sample and log2(1/pi) weights, shaped [rows, pages, 32].
+    """The sampled key blocks of every 128-query block and their weights.
 
-    ``descriptor``  - int32, sampled KV4 block ids, shape [rows, pages, 32].
-    ``log_weights`` - float32, log2 inverse-inclusion weights, same shape.
-
-    ``rows`` is batch * heads * ceil_div(tokens, 128); ``pages`` is
-    ``sample_pages``; each page packs 32 sampled KV4 blocks. Ids are local to
-    their head. Treat both tensors as read-only; build a new plan to refresh
-    the selection. (Reference: attention.py:11-23.)
+    ``descriptor`` holds int32 KV4-block indices counted within the block's
+    own (batch, head); ``log_weights`` holds the float32 logit shift of each
+    entry, log2 of its inverse inclusion probability (0 for blocks SIP kept
+    with certainty). Both are [rows, pages, 32]: one row per (batch, head,
+    query block) in that order, ``pages`` = ``sample_pages``, 32 blocks per
+    page. ``apply_plan`` only reads them, so one plan can serve several
+    calls; a new selection needs a new plan. (Reference: attention.py:11-23.)
     """
 
     descriptor: torch.Tensor
@@ -116,5 +116,7 @@ def apply_plan(q, k, v, plan, *, return_lse=False):
 
 @torch.no_grad()
 def ab_attention(q, k, v, *, sample_pages=64, seed=42):
-    """AB-Attention with a fresh sampling plan; output has Q's shape and dtype."""
+    """``build_plan`` then ``apply_plan`` in one call: sparse attention over
+    a freshly sampled plan, returned in q's shape and dtype
+    (reference: attention.py:99-102)."""
     return apply_plan(q, k, v, build_plan(q, k, sample_pages=sample_pages, seed=seed))

@@ -6,9 +6,8 @@ arithmetic is ``ab_paged_prefill_kv`` in libab_attention_hip.so: a bf16 MFMA
 flash-attention kernel that reads each row's KV4 blocks straight from K and
 V by their per-head ids and adds the SIP weight of each block to its logits
 (the reference's ABSipAttention variant, flashinfer_backend.py:30-59).
-``kv4_transpose`` produces the library's alternative V layout (each 4-key
-page stored dim-major, for ``ab_paged_prefill_kv4t``); it is not used here:
-on gfx950 it saves the prefill under 1 % and the transpose pass costs more.
+``_prefill_dense`` is the same kernel walking every KV4 block of K/V at
+weight 0, with no page list in memory (ab_dense_prefill).
 
 The reference translates per-head ids into a global page table and caches it
 per descriptor (flashinfer_backend.py:62-74, :202-217); the kernel here
@@ -28,19 +27,6 @@ from . import _lib
 _HEAD_DIM = 128
 _QUERY_BLOCK = 128
 _PAGE_SIZE = 4
-
-
-def kv4_transpose(v: torch.Tensor) -> torch.Tensor:
-    """V bf16 [B,H,Nk,128] (Nk % 4 == 0) -> the prefill's KV4-transposed layout
-    [B,H,Nk/4,128,4] (ab_kv4_transpose): each 4-key page stored dim-major, so
-    the kernel's PV operand reads are plain 8-byte LDS reads."""
-    v = v.contiguous()
-    batch, heads, tokens, dim = v.shape
-    out = torch.empty((batch, heads, tokens // _PAGE_SIZE, dim, _PAGE_SIZE), dtype=v.dtype, device=v.device)
-    lib = _lib.load()
-    with torch.cuda.device(v.device):
-        _lib.check(lib.ab_kv4_transpose(_lib.ptr(v), batch * heads, tokens, _lib.ptr(out), _lib.stream(v.device)))
-    return out
 
 
 def _prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
@@ -117,6 +103,22 @@ def _prefill_kv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ids: torch.Te
     weight removes its block). Shapes are checked by the callers.
     """
     return _prefill(q, k, v, ids, weights, None, return_lse)
+
+
+def _prefill_dense(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, return_lse: bool = False):
+    """Dense attention of q bf16 [B,H,Nq,128] over every key of k/v bf16
+    [B,H,Nk,128] (Nk % 4 == 0) on the prefill kernel (ab_dense_prefill); the
+    page list is implicit, so nothing of size rows x blocks is built. Shapes
+    are checked by the callers."""
+    batch, heads, tokens, _ = q.shape
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    output = torch.empty_like(q)
+    lse = torch.empty((batch, heads, tokens), dtype=torch.float32, device=q.device) if return_lse else None
+    lib = _lib.load()
+    with torch.cuda.device(q.device):
+        _lib.check(lib.ab_dense_prefill(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), batch * heads, tokens, k.shape[2],
+                                        _lib.ptr(output), _lib.ptr(lse), _lib.stream(q.device)))
+    return (output, lse) if return_lse else output
 
 
 def _remap_ids(ids: torch.Tensor, page_map: torch.Tensor) -> torch.Tensor:

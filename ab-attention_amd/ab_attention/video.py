@@ -26,7 +26,7 @@ import torch
 
 from . import _lib
 from .attention import SamplePlan, apply_plan, build_plan
-from .paged import _prefill_kv, _prefill_ordered, _remap_ids
+from .paged import _prefill_dense, _prefill_kv, _prefill_ordered, _remap_ids
 
 _QUERY_BLOCK = 128
 _PAGE = 4
@@ -161,12 +161,10 @@ def exact_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, return
     """Dense non-causal attention of q [B,H,Nq,128] over k/v [B,H,Nk,128]
     (bf16, Nk divisible by 4); returns o bf16 [B,H,Nq,128] (and the base-2
     lse f32 [B,H,Nq]). The reference's _exact (video.py:13-28) on this
-    library's prefill: every KV4 block of K/V listed at weight 0."""
+    library's prefill kernel walking every KV4 block of K/V at weight 0, with
+    no page list in memory (ab_dense_prefill)."""
     _check_qkv(q, k, v)
-    batch, heads, tokens, _ = q.shape
-    rows = batch * heads * math.ceil(tokens / _QUERY_BLOCK)
-    ids, weights = _dense_pages(rows, k.shape[2] // _PAGE, q.device)
-    return _prefill_kv(q, k, v, ids, weights, return_lse=return_lse)
+    return _prefill_dense(q, k, v, return_lse=return_lse)
 
 
 @torch.no_grad()
@@ -209,7 +207,7 @@ class VideoAttention:
         self.plans = {}
 
     def step_end(self, pipe, index, timestep, callback_kwargs):
-        self.step = index + 2  # Diffusers indices are zero-based.
+        self.step = index + 2  # the pipeline counts from 0, the schedule from 1
         return callback_kwargs
 
     def is_sparse(self, layer: int) -> bool:

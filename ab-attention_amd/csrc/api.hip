@@ -4,9 +4,14 @@
 // caller's stream, never synchronises and never allocates: buffers, including
 // workspace, belong to the caller. Failures return a nonzero status and leave
 // a message for ab_last_error().
+#include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <map>
+#include <mutex>
+#include <utility>
 
 #include "../../include/ab_attention.h"
 #include "common.hpp"
@@ -24,14 +29,12 @@ int launch_sip(const float* scores, const float* offsets, int64_t rows, int64_t 
                int32_t* ids, float* logw, hipStream_t stream);
 bool sip_fits(int64_t population);
 bool sip_fused_fits(int64_t population);
-void sip_force_exact_draws(int on);
 int launch_sip_fused(const void* lse, const float* pops, const float* lse_max, const float* lse_den, int64_t ld,
                      const float* offsets, int64_t rows, int64_t population, int64_t samples, int32_t* ids,
-                     float* logw, hipStream_t stream);
-int launch_prefill(const void* q, const void* k, const void* v, bool v_kv4t, int64_t bh, int64_t n, int64_t n_kv,
+                     float* logw, int force_exact, hipStream_t stream);
+int launch_prefill(const void* q, const void* k, const void* v, bool dense, int64_t bh, int64_t n, int64_t n_kv,
                    const int32_t* ids, const float* logw, int64_t samples, void* out, float* lse,
                    const int32_t* order, hipStream_t stream);
-int launch_kv4_transpose(const void* v, int64_t bh, int64_t n_kv, void* vt, hipStream_t stream);
 int launch_remap_ids(const int32_t* ids, int64_t count, const int32_t* map, int64_t map_len, int32_t* out,
                      hipStream_t stream);
 int launch_merge(const void* oa, const float* sa, const void* ob, const float* sb, int64_t count, void* out,
@@ -99,6 +102,39 @@ int check_launch(const char* what) {
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return set_error(AB_ERR_LAUNCH, "%s launch failed: %s", what, hipGetErrorString(err));
     return AB_OK;
+}
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_attr_mutex;
+std::map<std::pair<const void*, int>, int> g_lds_limit;  // (kernel, device) -> bytes set
+std::atomic<int> g_cu_count[kMaxDevices];
+}  // namespace
+
+int ensure_lds_limit(const void* fn, int bytes) {
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) return set_error(AB_ERR_LAUNCH, "no current HIP device");
+    std::lock_guard<std::mutex> lock(g_attr_mutex);
+    int& done = g_lds_limit[{fn, device}];
+    if (done >= bytes) return AB_OK;
+    const hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (err != hipSuccess)
+        return set_error(AB_ERR_LAUNCH, "setting a %d-byte LDS limit failed: %s", bytes, hipGetErrorString(err));
+    done = bytes;
+    return AB_OK;
+}
+
+int device_cu_count() {
+    int device = 0;
+    (void)hipGetDevice(&device);
+    if (device < 0 || device >= kMaxDevices) device = 0;
+    int cus = g_cu_count[device].load(std::memory_order_relaxed);
+    if (cus == 0) {
+        (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+        cus = std::max(cus, 1);
+        g_cu_count[device].store(cus, std::memory_order_relaxed);
+    }
+    return cus;
 }
 
 }  // namespace ab
@@ -203,9 +239,14 @@ size_t ab_ibcs_sip_workspace_bytes(int64_t batch_heads, int64_t tokens) {
     return ibcs_layout(batch_heads, tokens).total;
 }
 
-int ab_ibcs_sip(const void* q, const void* k, const int32_t* order, int64_t batch_heads, int64_t tokens,
-                const float* offsets, int64_t samples, void* workspace, size_t workspace_bytes, int32_t* ids,
-                float* log_weights, void* stream) {
+}  // extern "C"
+
+namespace {
+// ab_ibcs_sip; force_exact selects the reference's probe sequence for every
+// row sampled with kept prefixes (same bits, testing only).
+int ibcs_sip_impl(const void* q, const void* k, const int32_t* order, int64_t batch_heads, int64_t tokens,
+                  const float* offsets, int64_t samples, void* workspace, size_t workspace_bytes, int32_t* ids,
+                  float* log_weights, int force_exact, void* stream) {
     if (int rc = check_qk_shape("ibcs_sip", batch_heads, tokens)) return rc;
     const IbcsLayout L = ibcs_layout(batch_heads, tokens);
     if (!(samples > 0 && samples < L.fb))
@@ -232,7 +273,24 @@ int ab_ibcs_sip(const void* q, const void* k, const int32_t* order, int64_t batc
     if (int rc = launch_lse(ws + L.centroids, ws + L.pooled, batch_heads, tokens, ws + L.lse, lse_max, lse_den, st))
         return rc;
     return launch_sip_fused(ws + L.lse, pops, lse_max, lse_den, L.ld, offsets, L.rows, L.fb, samples, ids,
-                            log_weights, st);
+                            log_weights, force_exact, st);
+}
+}  // namespace
+
+extern "C" {
+
+int ab_ibcs_sip(const void* q, const void* k, const int32_t* order, int64_t batch_heads, int64_t tokens,
+                const float* offsets, int64_t samples, void* workspace, size_t workspace_bytes, int32_t* ids,
+                float* log_weights, void* stream) {
+    return ibcs_sip_impl(q, k, order, batch_heads, tokens, offsets, samples, workspace, workspace_bytes, ids,
+                         log_weights, 0, stream);
+}
+
+int ab_ibcs_sip_exact_draws(const void* q, const void* k, const int32_t* order, int64_t batch_heads,
+                            int64_t tokens, const float* offsets, int64_t samples, void* workspace,
+                            size_t workspace_bytes, int32_t* ids, float* log_weights, void* stream) {
+    return ibcs_sip_impl(q, k, order, batch_heads, tokens, offsets, samples, workspace, workspace_bytes, ids,
+                         log_weights, 1, stream);
 }
 
 int ab_sip(const float* scores, const float* offsets, int64_t rows, int64_t population, int64_t samples,
@@ -260,8 +318,9 @@ int ab_paged_prefill(const void* q, const void* k, const void* v, int64_t batch_
 }
 
 namespace {
-// Shared validation of the prefill entry points; v_kv4t selects V's layout.
-int paged_prefill_checked(const void* q, const void* k, const void* v, bool v_kv4t, const int32_t* order,
+// Shared validation of the prefill entry points. dense: every KV4 block of
+// K/V at weight 0 (ids and log_weights are not read; samples is derived).
+int paged_prefill_checked(const void* q, const void* k, const void* v, bool dense, const int32_t* order,
                           int64_t batch_heads, int64_t q_tokens, int64_t kv_tokens, const int32_t* ids,
                           const float* log_weights, int64_t samples, void* out, float* lse, void* stream) {
     if (batch_heads <= 0 || q_tokens <= 0 || kv_tokens <= 0)
@@ -272,17 +331,18 @@ int paged_prefill_checked(const void* q, const void* k, const void* v, bool v_kv
         return set_error(AB_ERR_INVALID, "paged_prefill: one head of K/V must be under 4 GiB");
     const int64_t qb = (q_tokens + kQueryBlock - 1) / kQueryBlock;
     if (batch_heads > 65535 || qb > 65535) return set_error(AB_ERR_INVALID, "paged_prefill: grid too large");
+    if (dense) samples = (kv_tokens / kKvBlock + 7) / 8 * 8;
     if (samples <= 0 || samples % 8)
         return set_error(AB_ERR_INVALID, "paged_prefill: samples must be a positive multiple of 8");
-    if (!q || !k || !v || !ids || !log_weights || !out)
+    if (!q || !k || !v || !out || (!dense && (!ids || !log_weights)))
         return set_error(AB_ERR_INVALID, "paged_prefill: null pointer");
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || (reinterpret_cast<uintptr_t>(out) & 7u))
         return set_error(AB_ERR_INVALID, "paged_prefill: q/k/v must be 16-byte and out 8-byte aligned");
-    if (!aligned16(ids) || !aligned16(log_weights))
+    if (!dense && (!aligned16(ids) || !aligned16(log_weights)))
         return set_error(AB_ERR_INVALID, "paged_prefill: ids and log_weights must be 16-byte aligned");
     const int64_t rows = batch_heads * qb;
     if (rows * samples > (int64_t(1) << 40)) return set_error(AB_ERR_INVALID, "paged_prefill: plan too large");
-    return launch_prefill(q, k, v, v_kv4t, batch_heads, q_tokens, kv_tokens, ids, log_weights, samples, out, lse,
+    return launch_prefill(q, k, v, dense, batch_heads, q_tokens, kv_tokens, ids, log_weights, samples, out, lse,
                           order, static_cast<hipStream_t>(stream));
 }
 }  // namespace
@@ -294,6 +354,12 @@ int ab_paged_prefill_kv(const void* q, const void* k, const void* v, int64_t bat
                                  samples, out, lse, stream);
 }
 
+int ab_dense_prefill(const void* q, const void* k, const void* v, int64_t batch_heads, int64_t q_tokens,
+                     int64_t kv_tokens, void* out, float* lse, void* stream) {
+    return paged_prefill_checked(q, k, v, true, nullptr, batch_heads, q_tokens, kv_tokens, nullptr, nullptr, 0,
+                                 out, lse, stream);
+}
+
 int ab_paged_prefill_ordered(const void* q, const void* k, const void* v, const int32_t* order,
                              int64_t batch_heads, int64_t tokens, const int32_t* ids, const float* log_weights,
                              int64_t samples, void* out, float* lse, void* stream) {
@@ -303,25 +369,6 @@ int ab_paged_prefill_ordered(const void* q, const void* k, const void* v, const 
         return set_error(AB_ERR_INVALID, "paged_prefill: samples must be a positive multiple of 32");
     return paged_prefill_checked(q, k, v, false, order, batch_heads, tokens, tokens, ids, log_weights, samples,
                                  out, lse, stream);
-}
-
-int ab_kv4_transpose(const void* v, int64_t batch_heads, int64_t kv_tokens, void* v_kv4t, void* stream) {
-    if (batch_heads < 0 || kv_tokens < 0 || kv_tokens % kKvBlock)
-        return set_error(AB_ERR_INVALID, "kv4_transpose: bad shape (kv_tokens must be divisible by 4)");
-    if (batch_heads * kv_tokens == 0) return AB_OK;
-    if (!v || !v_kv4t) return set_error(AB_ERR_INVALID, "kv4_transpose: null pointer");
-    if (!aligned16(v) || !aligned16(v_kv4t))
-        return set_error(AB_ERR_INVALID, "kv4_transpose: buffers must be 16-byte aligned");
-    if (batch_heads * (kv_tokens / kKvBlock) * 16 > (int64_t(0xffffffff) * 256))
-        return set_error(AB_ERR_INVALID, "kv4_transpose: too large");
-    return launch_kv4_transpose(v, batch_heads, kv_tokens, v_kv4t, static_cast<hipStream_t>(stream));
-}
-
-int ab_paged_prefill_kv4t(const void* q, const void* k, const void* v_kv4t, const int32_t* order,
-                          int64_t batch_heads, int64_t q_tokens, int64_t kv_tokens, const int32_t* ids,
-                          const float* log_weights, int64_t samples, void* out, float* lse, void* stream) {
-    return paged_prefill_checked(q, k, v_kv4t, true, order, batch_heads, q_tokens, kv_tokens, ids, log_weights,
-                                 samples, out, lse, stream);
 }
 
 int ab_remap_ids(const int32_t* ids, int64_t count, const int32_t* map, int64_t map_len, int32_t* out,
@@ -342,11 +389,6 @@ int ab_merge_states(const void* o_a, const float* lse_a, const void* o_b, const 
         return set_error(AB_ERR_INVALID, "merge_states: states must be 16-byte aligned");
     if (count > (int64_t(1) << 35)) return set_error(AB_ERR_INVALID, "merge_states: too many rows");
     return launch_merge(o_a, lse_a, o_b, lse_b, count, out, lse_out, static_cast<hipStream_t>(stream));
-}
-
-int ab_testing_force_exact_draws(int on) {
-    sip_force_exact_draws(on);
-    return AB_OK;
 }
 
 }  // extern "C"

@@ -70,4 +70,11 @@ __device__ __forceinline__ void lds_barrier() {
 namespace ab {
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
+// Raises the dynamic-LDS limit of kernel `fn` on the current device to at
+// least `bytes`. The attribute is per device; each (kernel, device) pair is
+// set once, so later launches (including launches recorded into a HIP graph)
+// make no attribute call. Returns 0, or a nonzero status on failure.
+int ensure_lds_limit(const void* fn, int bytes);
+// Compute units of the current device (cached per device).
+int device_cu_count();
 }  // namespace ab

@@ -402,9 +402,7 @@ int launch_lse(const void* centroids, const void* pooled, int64_t bh, int64_t n,
     const int64_t total = groups_per_head * bh;
     if (total > (int64_t(1) << 30)) return set_error(1, "ibcs: too many query blocks (%lld)", (long long)total);
     const int per_xcd = static_cast<int>((total + 7) / 8);
-    // The attribute is per device: set it on every launch (a host-side call).
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(lse_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              kLseLdsBytes);
+    if (int rc = ensure_lds_limit(reinterpret_cast<const void*>(lse_kernel), kLseLdsBytes)) return rc;
     hipLaunchKernelGGL(lse_kernel, dim3(static_cast<unsigned>(per_xcd * 8)), dim3(kLseThreads), kLseLdsBytes,
                        stream, static_cast<const uint16_t*>(centroids), static_cast<const uint16_t*>(pooled),
                        static_cast<_Float16*>(lse), lse_max, lse_den, qb, static_cast<int>(fb), lse_stride(fb),

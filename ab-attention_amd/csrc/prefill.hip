@@ -94,14 +94,10 @@ __device__ __forceinline__ void wait_and_barrier() {
     asm volatile("s_barrier" ::: "memory");
 }
 
-// kVT selects the layout of V:
-//   false: row-major [n_kv, 128], read with the transposing LDS read (the
-//          tile is swizzled so those reads are conflict free);
-//   true:  KV4-transposed [n_kv/4, 128, 4] (kv4_transpose_kernel): each page
-//          is 128 dims x 4 keys, so the PV operand of a lane (one dim, 8 keys
-//          from two pages) is two plain 8-byte LDS reads, at twice the rate
-//          of the transposing read on gfx950.
-template <bool kVT>
+// kDense: every KV4 block of K/V in order (tile u holds blocks 8u .. 8u+7)
+// at weight 0, blocks past the end at -inf; ids and logw are not read. This
+// is dense attention with no page list in memory.
+template <bool kDense>
 __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const int32_t* __restrict__ ids, const float* __restrict__ logw, uint16_t* __restrict__ out,
@@ -184,7 +180,6 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
         k_src[e] = uint32_t(r * 16 + (pos ^ (key & 15))) * 16u;
     }
     const uint32_t v_src = [&] {
-        if (kVT) return uint32_t(lane) * 16u;
         const int m = lane >> 3, sl = (lane >> 1) & 3, h = lane & 1;
         return uint32_t((sl ^ ((m >> 1) & 3)) * 16 + 2 * m + h) * 16u;
     }();
@@ -193,6 +188,11 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
     // last tile (their transfers only keep the per-step count uniform).
     auto load_ids = [&](int u) {
         const int uc = min(u, tiles - 1);
+        if (kDense) {
+            const int id = uc * kTilePages + 2 * wave;
+            const u32x2 c = {uint32_t(min(id, fb - 1)), uint32_t(min(id + 1, fb - 1))};
+            return c;
+        }
         const u32x2 raw = *reinterpret_cast<const u32x2*>(smem + kIdsOffset + ((uc / kBatchTiles) & 1) * kBatchBytes +
                                                           ((uc % kBatchTiles) * kTilePages + 2 * wave) * 4);
         const u32x2 c = {uint32_t(min(max(static_cast<int>(raw[0]), 0), fb - 1)),
@@ -209,6 +209,11 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
     // holds key 8*(r/4) + 4*half + r%4, i.e. page 2(r/4) + half.
     auto load_weights = [&](int u, float (&wv)[4]) {
         const int uc = min(u, tiles - 1);
+        if (kDense) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) wv[g] = uc * kTilePages + 2 * g + half < fb ? 0.f : -INFINITY;
+            return;
+        }
         const float* ws = reinterpret_cast<const float*>(smem + kWeightsOffset +
                                                          ((uc / kBatchTiles) & 1) * kBatchBytes) +
                           (uc % kBatchTiles) * kTilePages;
@@ -243,20 +248,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
     // half, on both operands. Lane (group g = lane/16, i = lane%16) does two
     // transposing reads; the source lane 4r + q addresses key r of that page,
     // dims 32dt + 16(g%2) + 4q .. +3, so lane i receives dim 32dt + 16(g%2) + i.
-    // KV4-transposed V: lane (dim 32dt + qi, half) reads that dim's 4 keys of
-    // tile pages 4ks + half (t = 0) and 4ks + 2 + half (t = 1). The two reads
-    // use separate base registers so they stay two ds_read_b64 (a merged
-    // ds_read2st64_b64 is slower).
-    const uint32_t vt0 = kVRing + half * 1024 + qi * 8;
-    uint32_t vt1 = vt0 + 2048;
-    asm volatile("" : "+v"(vt1));
     auto read_v = [&](int u, int j) {
-        if (kVT) {
-            const int off = (u & (kRing - 1)) * kTileBytes + (j >> 2) * 4096 + (j & 3) * 256;
-            const u32x2 lo = *reinterpret_cast<const u32x2*>(smem + vt0 + off);
-            const u32x2 hi = *reinterpret_cast<const u32x2*>(smem + vt1 + off);
-            return __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
-        }
         const uint32_t a0 = v_abs[j & 3] + (u & (kRing - 1)) * kTileBytes + (j >> 2) * 4096;
         const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_i16x4*>(static_cast<uintptr_t>(a0)));
         const i16x4 hi =
@@ -269,7 +261,12 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o_acc[dt][r] = 0.f;
-    float m_run = 0.f, l_run = 0.f;  // reference set by the first tile
+    // The reference is set by the first tile that holds a finite logit for
+    // this query (`started`); tiles before it (every block at weight -inf)
+    // contribute nothing. mx is the same in both lane halves of a query, so
+    // `started` and m_run are too.
+    float m_run = 0.f, l_run = 0.f;
+    bool started = false;
 
     // Step t works on three tiles at once, so that every MFMA of the wave has
     // independent VALU and LDS work beside it. Entering step t, sc holds the
@@ -292,16 +289,20 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
     auto step = [&](int t, f32x16& sc, f32x16& sn, float& mx, u32x4 (&ka)[8], float (&wn)[4], u32x2& idk,
                     u32x2& idv) {
         wait_and_barrier<2 * kGroupOps>();
-        if (wave == 0 && t % kBatchTiles == kBatchTiles / 2 && (t / kBatchTiles + 1) * kBatchTiles < tiles)
+        if (!kDense && wave == 0 && t % kBatchTiles == kBatchTiles / 2 && (t / kBatchTiles + 1) * kBatchTiles < tiles)
             issue_batch(t / kBatchTiles + 1);
         {
             const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
             mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
         }
-        const bool grow = t == 0 || mx > kSlack;
+        const bool was_started = started;
+        const bool grow = was_started ? mx > kSlack : mx > -INFINITY;
+        started = was_started || grow;
         if (__any(grow)) {
             const float shift = grow ? mx : 0.f;
-            const float alpha = fast_exp2(-shift);
+            // l_run and O are still zero before the first move, so alpha is
+            // left at 1 there (2^-mx could overflow for a very negative mx).
+            const float alpha = was_started ? fast_exp2(-shift) : 1.f;
             m_run += shift;
             l_run *= alpha;
 #pragma unroll
@@ -366,7 +367,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
     // are in; K(4) goes into K(0)'s stage only after every wave has read it.
     // The last eight transfers before step 0 are then K(3), V(1), V(2), K(4),
     // as step 0's wait expects.
-    if (wave == 0) issue_batch(0);
+    if (!kDense && wave == 0) issue_batch(0);
     wait_and_barrier<0>();
     {
 #pragma unroll
@@ -441,7 +442,9 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
     const auto lsw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
     const float l_tot = __uint_as_float(lsw[0]) + __uint_as_float(lsw[1]);
     if (valid_q) {
-        const float inv = 1.0f / l_tot;
+        // A query whose every listed block has weight -inf gets o = 0 and
+        // lse = -inf.
+        const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
         uint16_t* orow = out + (bh * n + qrow_index) * kHeadDim;
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt)
@@ -451,31 +454,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
                                   pack_bf16(o_acc[dt][4 * g + 2] * inv, o_acc[dt][4 * g + 3] * inv)};
                 *reinterpret_cast<u32x2*>(orow + 32 * dt + 8 * g + 4 * half) = pk;
             }
-        if (lse != nullptr && half == 0) lse[bh * n + qrow_index] = m_run + log2f(l_tot);
-    }
-}
-
-// V [bh, n_kv, 128] -> KV4-transposed [bh, n_kv/4, 128, 4]: page j holds, for
-// each dim d, keys 4j..4j+3 (8 bytes). One thread per (page, 8 dims): four
-// 16-byte row reads, four 16-byte writes (64 contiguous bytes).
-__global__ __launch_bounds__(256) void kv4_transpose_kernel(const uint32_t* __restrict__ v, int64_t pages,
-                                                            uint32_t* __restrict__ vt) {
-    const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    const int64_t page = idx >> 4;
-    const int c = static_cast<int>(idx & 15);
-    if (page >= pages) return;
-    u32x4 in[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) in[r] = reinterpret_cast<const u32x4*>(v + (page * 4 + r) * 64)[c];
-    u32x4* dst = reinterpret_cast<u32x4*>(vt + page * 256 + c * 16);
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        // dims 8c + 2m (low halves of word m) and 8c + 2m + 1 (high halves)
-        const u32x4 o = {__builtin_amdgcn_perm(in[1][m], in[0][m], 0x05040100u),
-                         __builtin_amdgcn_perm(in[3][m], in[2][m], 0x05040100u),
-                         __builtin_amdgcn_perm(in[1][m], in[0][m], 0x07060302u),
-                         __builtin_amdgcn_perm(in[3][m], in[2][m], 0x07060302u)};
-        dst[m] = o;
+        if (lse != nullptr && half == 0) lse[bh * n + qrow_index] = started ? m_run + log2f(l_tot) : -INFINITY;
     }
 }
 
@@ -532,15 +511,6 @@ int launch_merge(const void* oa, const float* sa, const void* ob, const float* s
     return check_launch("merge_kernel");
 }
 
-int launch_kv4_transpose(const void* v, int64_t bh, int64_t n_kv, void* vt, hipStream_t stream) {
-    const int64_t pages = bh * (n_kv / kKvBlock);
-    if (pages == 0) return 0;
-    const int64_t threads = pages * 16;
-    hipLaunchKernelGGL(kv4_transpose_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, stream,
-                       static_cast<const uint32_t*>(v), pages, static_cast<uint32_t*>(vt));
-    return check_launch("kv4_transpose_kernel");
-}
-
 int launch_remap_ids(const int32_t* ids, int64_t count, const int32_t* map, int64_t map_len, int32_t* out,
                      hipStream_t stream) {
     if (count == 0) return 0;
@@ -550,24 +520,22 @@ int launch_remap_ids(const int32_t* ids, int64_t count, const int32_t* map, int6
     return check_launch("remap_ids_kernel");
 }
 
-int launch_prefill(const void* q, const void* k, const void* v, bool v_kv4t, int64_t bh, int64_t n, int64_t n_kv,
+int launch_prefill(const void* q, const void* k, const void* v, bool dense, int64_t bh, int64_t n, int64_t n_kv,
                    const int32_t* ids, const float* logw, int64_t samples, void* out, float* lse,
                    const int32_t* order, hipStream_t stream) {
     const int64_t qb = (n + kQueryBlock - 1) / kQueryBlock;
     const int64_t rows = bh * qb;
     if (samples % kTilePages != 0)
         return set_error(1, "prefill: samples (%lld) must be a multiple of %d", (long long)samples, kTilePages);
-    if ((reinterpret_cast<uintptr_t>(ids) & 15u) || (reinterpret_cast<uintptr_t>(logw) & 15u))
+    if (!dense && ((reinterpret_cast<uintptr_t>(ids) & 15u) || (reinterpret_cast<uintptr_t>(logw) & 15u)))
         return set_error(1, "prefill: ids and log_weights must be 16-byte aligned");
     if (n_kv * kHeadDim * 2 > int64_t(0xffffffff))
         return set_error(1, "prefill: one head of K/V must be under 4 GiB");
     const float scale_log2 = static_cast<float>(1.4426950408889634 / 11.313708498984761);  // log2(e)/sqrt(128)
     const int64_t per_xcd = (qb + 7) / 8;
     if (rows == 0) return 0;
-    auto kernel = v_kv4t ? prefill_kernel<true> : prefill_kernel<false>;
-    // The attribute is per device: set it on every launch (a host-side call).
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              kLdsBytes);
+    auto kernel = dense ? prefill_kernel<true> : prefill_kernel<false>;
+    if (int rc = ensure_lds_limit(reinterpret_cast<const void*>(kernel), kLdsBytes)) return rc;
     hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(per_xcd * 8 * bh)), dim3(kPfThreads), kLdsBytes,
                        stream, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                        static_cast<const uint16_t*>(v), ids, logw, static_cast<uint16_t*>(out), lse, n, n_kv, qb, rows,
@@ -576,4 +544,3 @@ int launch_prefill(const void* q, const void* k, const void* v, bool v_kv4t, int
 }
 
 }  // namespace ab
-

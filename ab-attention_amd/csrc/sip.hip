@@ -799,13 +799,11 @@ template <int kPer>
 int launch_lds(const float* scores, const float* offsets, int64_t rows, int pop, int samples, int32_t* ids,
                float* logw, size_t bytes, hipStream_t stream) {
     const void* fn = reinterpret_cast<const void*>(sip_lds_kernel<kPer>);
-    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
-    int device = 0, cus = 0, per_cu = 0;
-    (void)hipGetDevice(&device);
-    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+    if (int rc = ensure_lds_limit(fn, static_cast<int>(bytes))) return rc;
+    int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kSipWorkers, bytes) != hipSuccess || per_cu < 1)
         per_cu = 1;
-    const int64_t grid = std::min<int64_t>(rows, int64_t(std::max(cus, 1)) * per_cu);
+    const int64_t grid = std::min<int64_t>(rows, int64_t(device_cu_count()) * per_cu);
     hipLaunchKernelGGL(sip_lds_kernel<kPer>, dim3(static_cast<unsigned>(grid)), dim3(kSipWorkers), bytes, stream,
                        scores, offsets, ids, logw, pop, samples, rows);
     return check_launch("sip_lds_kernel");
@@ -837,46 +835,43 @@ bool sip_fused_fits(int64_t population) {
 static_assert(sip_fused_coarse_offset(kMaxKvBlocks) + 2 * kSipThreads * sizeof(double) + kSipStaticLds <= kLdsLimit,
               "every row the API accepts fits the fused kernel's LDS");
 
-// Testing hook: every row sampled with kept prefixes takes the reference's
-// probe sequence (the path otherwise used only when a threshold lands in a
-// rounding drop of the prefix array, which the tests cannot construct).
-static int g_force_exact = 0;
-void sip_force_exact_draws(int on) { g_force_exact = on != 0; }
-
 namespace {
 
 template <bool kCoarse>
 int launch_fused(const _Float16* lse, const float* pops, const float* lse_max, const float* lse_den, int64_t ld,
                  const float* offsets, int64_t rows, int pop, int samples, int32_t* ids, float* logw,
-                 hipStream_t stream) {
+                 int force_exact, hipStream_t stream) {
     const size_t bytes = sip_fused_lds_bytes(pop, kCoarse);
     const void* fn = reinterpret_cast<const void*>(sip_fused_kernel<kCoarse>);
-    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
-    int device = 0, cus = 0, per_cu = 0;
-    (void)hipGetDevice(&device);
-    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+    if (int rc = ensure_lds_limit(fn, static_cast<int>(bytes))) return rc;
+    int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kSipWorkers, bytes) != hipSuccess || per_cu < 1)
         per_cu = 1;
-    const int64_t grid = std::min<int64_t>(rows, int64_t(std::max(cus, 1)) * per_cu);
+    const int64_t grid = std::min<int64_t>(rows, int64_t(device_cu_count()) * per_cu);
     hipLaunchKernelGGL(sip_fused_kernel<kCoarse>, dim3(static_cast<unsigned>(grid)), dim3(kSipWorkers), bytes,
                        stream, lse, pops, lse_max, lse_den, ld, offsets, ids, logw, pop, samples, rows,
-                       g_force_exact);
+                       force_exact);
     return check_launch("sip_fused_kernel");
 }
 
 }  // namespace
 
+// force_exact: every row sampled with kept prefixes takes the reference's
+// probe sequence (the path otherwise used only when a threshold lands in a
+// rounding drop of the prefix array, which tests cannot construct); the bits
+// are the same either way.
 int launch_sip_fused(const void* lse, const float* pops, const float* lse_max, const float* lse_den, int64_t ld,
                      const float* offsets, int64_t rows, int64_t population, int64_t samples, int32_t* ids,
-                     float* logw, hipStream_t stream) {
+                     float* logw, int force_exact, hipStream_t stream) {
     if (!sip_fused_fits(population))
         return set_error(1, "sip: population %lld does not fit the fused kernel's LDS", (long long)population);
     if (rows == 0) return 0;
     const _Float16* h = static_cast<const _Float16*>(lse);
     const int pop = static_cast<int>(population), s = static_cast<int>(samples);
     if (sip_fused_lds_bytes(population, false) + kSipStaticLds <= kLdsLimit)
-        return launch_fused<false>(h, pops, lse_max, lse_den, ld, offsets, rows, pop, s, ids, logw, stream);
-    return launch_fused<true>(h, pops, lse_max, lse_den, ld, offsets, rows, pop, s, ids, logw, stream);
+        return launch_fused<false>(h, pops, lse_max, lse_den, ld, offsets, rows, pop, s, ids, logw, force_exact,
+                                   stream);
+    return launch_fused<true>(h, pops, lse_max, lse_den, ld, offsets, rows, pop, s, ids, logw, force_exact, stream);
 }
 
 int launch_sip(const float* scores, const float* offsets, int64_t rows, int64_t population, int64_t samples,
@@ -894,8 +889,8 @@ int launch_sip(const float* scores, const float* offsets, int64_t rows, int64_t 
         if (per_thread <= 24) return launch_lds<24>(scores, offsets, rows, pop, s, ids, logw, lds_bytes, stream);
     }
     const size_t bytes = sip_lds_bytes(population, false);
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(sip_global_kernel),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+    if (int rc = ensure_lds_limit(reinterpret_cast<const void*>(sip_global_kernel), static_cast<int>(bytes)))
+        return rc;
     hipLaunchKernelGGL(sip_global_kernel, dim3(static_cast<unsigned>(rows)), dim3(kSipWorkers), bytes, stream,
                        scores, offsets, ids, logw, pop, s);
     return check_launch("sip_global_kernel");

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define AB_ABI_VERSION 2
+#define AB_ABI_VERSION 3
 
 enum ab_status {
     AB_OK = 0,
@@ -89,12 +89,15 @@ int ab_ibcs_sip(const void *q, const void *k, const int32_t *order, int64_t batc
                 const float *offsets, int64_t samples, void *workspace, size_t workspace_bytes, int32_t *ids,
                 float *log_weights, void *stream);
 
-/* Testing hook; no counterpart in the reference. With `on` nonzero, every row
- * that ab_ibcs_sip samples with kept prefixes takes the reference's
- * binary-search probes (each prefix rebuilt from the kept ones), the path
- * otherwise taken only when a threshold lands in a rounding drop of the
- * prefix array. The bits are the same either way. Process-wide; returns 0. */
-int ab_testing_force_exact_draws(int on);
+/* Testing variant of ab_ibcs_sip; no counterpart in the reference. Every
+ * row that is sampled with kept prefixes takes the reference's binary-search
+ * probes (each prefix rebuilt from the kept ones), the path otherwise taken
+ * only when a threshold lands in a rounding drop of the prefix array, which
+ * no test input can be built to hit. The ids and weights are the same bits
+ * as ab_ibcs_sip's; the tests compare the two. */
+int ab_ibcs_sip_exact_draws(const void *q, const void *k, const int32_t *order, int64_t batch_heads,
+                            int64_t tokens, const float *offsets, int64_t samples, void *workspace,
+                            size_t workspace_bytes, int32_t *ids, float *log_weights, void *stream);
 
 /* ---- Weighted paged prefill ------------------------------------------------
  * Replaces the FlashInfer FA3 run with the ABSipAttention variant
@@ -110,29 +113,23 @@ int ab_paged_prefill(const void *q, const void *k, const void *v, int64_t batch_
 
 /* The same prefill with a K/V length of its own (kv_tokens, divisible by 4)
  * and any positive multiple of 8 for samples (a listed block may carry a
- * -inf weight, which removes it). With every block of K/V listed at weight 0
- * this is dense attention: it replaces the FA3 single prefill of _exact
- * (ab_attention/video.py:13-28); with a plan's ids plus the text blocks at
+ * -inf weight, which removes it; a query whose every listed block is at -inf
+ * gets o = 0 and lse = -inf). With a plan's ids plus the text blocks at
  * weight 0 it computes _hunyuan_attention's video state and its merge with
- * the exact text state in one pass (video.py:129-142). */
+ * the exact text state in one pass (ab_attention/video.py:129-142). */
 int ab_paged_prefill_kv(const void *q, const void *k, const void *v, int64_t batch_heads, int64_t q_tokens,
                         int64_t kv_tokens, const int32_t *ids, const float *log_weights, int64_t samples,
                         void *out, float *lse, void *stream);
 
-/* ---- KV4-transposed V (the prefill's fast V layout) -------------------------
- * No counterpart in the reference: FlashInfer reads V as [pages, 4, 1, 128]
- * (ab_attention/flashinfer_backend.py:219-230). ab_kv4_transpose writes v bf16
- * [batch_heads, kv_tokens, 128] (kv_tokens divisible by 4) as v_kv4t bf16
- * [batch_heads, kv_tokens / 4, 128, 4]: page j holds, for each dim, keys
- * 4j..4j+3. Same size as v; buffers 16-byte aligned.
- * ab_paged_prefill_kv4t is ab_paged_prefill_kv over that layout, with an
- * optional token order (NULL: identity; otherwise as ab_paged_prefill_ordered,
- * order int32 [q_tokens]). It produces bit-identical results to the row-major
- * entry points on the same inputs. */
-int ab_kv4_transpose(const void *v, int64_t batch_heads, int64_t kv_tokens, void *v_kv4t, void *stream);
-int ab_paged_prefill_kv4t(const void *q, const void *k, const void *v_kv4t, const int32_t *order,
-                          int64_t batch_heads, int64_t q_tokens, int64_t kv_tokens, const int32_t *ids,
-                          const float *log_weights, int64_t samples, void *out, float *lse, void *stream);
+/* Dense attention of q [batch_heads, q_tokens, 128] over every key of k, v
+ * [batch_heads, kv_tokens, 128] (kv_tokens divisible by 4), with the base-2
+ * lse if lse != NULL: ab_paged_prefill_kv with every KV4 block listed at
+ * weight 0, without a page list in memory (the kernel walks the blocks in
+ * order). Replaces the FA3 single prefill of _exact
+ * (ab_attention/video.py:13-28), which runs steps 1-10 and layer 0 of a
+ * video (README.md:132-133). */
+int ab_dense_prefill(const void *q, const void *k, const void *v, int64_t batch_heads, int64_t q_tokens,
+                     int64_t kv_tokens, void *out, float *lse, void *stream);
 
 /* ---- Attention-state merge -------------------------------------------------
  * Replaces FlashInfer's merge_state as used by _merge

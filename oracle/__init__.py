@@ -5,7 +5,9 @@ the ``cpu_baseline`` leg of ``bench.py`` as the checker. The product path
 (``ab_attention``) never imports it.
 
 The arithmetic lives in ``ab_oracle.c`` (built by ``oracle/Makefile`` into
-``liboracle.so``); this module converts torch/numpy arrays and calls it.
+``liboracle.so``); this module converts torch/numpy arrays and calls it. Row
+loops run on OpenMP threads (``OMP_NUM_THREADS``); every row is computed by
+one thread in a fixed order, so results do not depend on the thread count.
 Reference call sites restated (paths relative to the reference checkout):
 ``csrc/ibcs.cu:106-538`` (IBCS), ``csrc/sip.cu:33-167`` (SIP),
 ``ab_attention/flashinfer_backend.py:30-59`` (weighted prefill).
@@ -67,7 +69,14 @@ def lib():
         _lib.orc_f16_to_f32.restype = ctypes.c_float
         _lib.orc_f32_to_bf16.argtypes = [ctypes.c_float]
         _lib.orc_f32_to_bf16.restype = ctypes.c_uint16
+        _lib.orc_num_threads.argtypes = []
+        _lib.orc_num_threads.restype = ctypes.c_int
     return _lib
+
+
+def num_threads() -> int:
+    """Host threads the oracle's row loops run on (OpenMP)."""
+    return int(lib().orc_num_threads())
 
 
 def _ptr(a: np.ndarray):

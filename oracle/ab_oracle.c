@@ -16,10 +16,14 @@
  *   orc_sip       csrc/sip.cu:33-167
  *   orc_prefill   ab_attention/flashinfer_backend.py:30-59, :164-242
  *
- * Build: oracle/Makefile (gcc -O2 -ffp-contract=off). Contraction is off so
- * that every fused multiply-add below is one the restatement asks for with
- * fmaf()/fma(), mirroring where nvcc's default contraction fuses `a += b * c`
- * in the reference build.
+ * Build: oracle/Makefile (gcc -O2 -ffp-contract=off -fopenmp). Contraction
+ * is off so that every fused multiply-add below is one the restatement asks
+ * for with fmaf()/fma(), mirroring where nvcc's default contraction fuses
+ * `a += b * c` in the reference build.
+ *
+ * Rows (query blocks) are independent in every stage, so the row loops run
+ * in parallel over OpenMP threads; each row is computed by one thread in the
+ * order written here, so the results do not depend on the thread count.
  *
  * Deliberate restatement choices (the reference build uses --use_fast_math,
  * whose approximate division/exp2/log2 are not reproduced):
@@ -29,6 +33,9 @@
  *     multiplication by its reciprocal, computed once per (row, centroid).
  */
 #include <float.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
@@ -99,6 +106,15 @@ uint16_t orc_f32_to_f16(float f) { return f32_to_f16(f); }
 float orc_f16_to_f32(uint16_t h) { return f16_to_f32(h); }
 uint16_t orc_f32_to_bf16(float f) { return f32_to_bf16(f); }
 
+/* Threads the parallel row loops use (OMP_NUM_THREADS, else all host threads). */
+int orc_num_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
 /* ---- IBCS stage 1: query clustering (csrc/ibcs.cu:106-238) -------------- */
 
 /*
@@ -145,50 +161,50 @@ static int argmax_lowest(const float *v, int valid) {
 void orc_cluster(const uint16_t *q, int64_t bh_count, int64_t n, float qk_scale_log2,
                  uint16_t *centroids, float *pops) {
     const int64_t qb = (n + QUERY_BLOCK - 1) / QUERY_BLOCK;
-    static float x[QUERY_BLOCK][HEAD_DIM];
-    float mean[HEAD_DIM], min_d[QUERY_BLOCK];
-    int assign[QUERY_BLOCK];
-    for (int64_t bh = 0; bh < bh_count; ++bh) {
-        for (int64_t blk = 0; blk < qb; ++blk) {
-            const int64_t base = blk * QUERY_BLOCK;
-            const int valid = (int)((n - base) < QUERY_BLOCK ? (n - base) : QUERY_BLOCK);
-            for (int i = 0; i < valid; ++i)
-                for (int d = 0; d < HEAD_DIM; ++d)
-                    x[i][d] = bf16_to_f32(q[((bh * n) + base + i) * HEAD_DIM + d]);
-            for (int d = 0; d < HEAD_DIM; ++d) {
-                float sum = 0.0f;
-                for (int i = 0; i < valid; ++i) sum += x[i][d];
-                mean[d] = sum / (float)valid;
-            }
-            for (int i = 0; i < valid; ++i) min_d[i] = lane_distance(x[i], mean);
-            int center = argmax_lowest(min_d, valid);
+#pragma omp parallel for schedule(dynamic, 8)
+    for (int64_t row_index = 0; row_index < bh_count * qb; ++row_index) {
+        const int64_t bh = row_index / qb, blk = row_index % qb;
+        float x[QUERY_BLOCK][HEAD_DIM];
+        float mean[HEAD_DIM], min_d[QUERY_BLOCK];
+        int assign[QUERY_BLOCK];
+        const int64_t base = blk * QUERY_BLOCK;
+        const int valid = (int)((n - base) < QUERY_BLOCK ? (n - base) : QUERY_BLOCK);
+        for (int i = 0; i < valid; ++i)
+            for (int d = 0; d < HEAD_DIM; ++d)
+                x[i][d] = bf16_to_f32(q[((bh * n) + base + i) * HEAD_DIM + d]);
+        for (int d = 0; d < HEAD_DIM; ++d) {
+            float sum = 0.0f;
+            for (int i = 0; i < valid; ++i) sum += x[i][d];
+            mean[d] = sum / (float)valid;
+        }
+        for (int i = 0; i < valid; ++i) min_d[i] = lane_distance(x[i], mean);
+        int center = argmax_lowest(min_d, valid);
+        for (int i = 0; i < valid; ++i) {
+            min_d[i] = INFINITY;
+            assign[i] = 0;
+        }
+        for (int slot = 0; slot < CENTROIDS; ++slot) {
             for (int i = 0; i < valid; ++i) {
-                min_d[i] = INFINITY;
-                assign[i] = 0;
-            }
-            for (int slot = 0; slot < CENTROIDS; ++slot) {
-                for (int i = 0; i < valid; ++i) {
-                    const float dist = lane_distance(x[i], x[center]);
-                    if (dist < min_d[i]) {
-                        min_d[i] = dist;
-                        assign[i] = slot;
-                    }
+                const float dist = lane_distance(x[i], x[center]);
+                if (dist < min_d[i]) {
+                    min_d[i] = dist;
+                    assign[i] = slot;
                 }
-                if (slot + 1 < CENTROIDS) center = argmax_lowest(min_d, valid);
             }
-            int counts[CENTROIDS] = {0};
-            for (int i = 0; i < valid; ++i) ++counts[assign[i]];
-            const int64_t row = bh * qb + blk;
-            for (int s = 0; s < CENTROIDS; ++s) pops[row * CENTROIDS + s] = (float)counts[s];
-            for (int d = 0; d < HEAD_DIM; ++d) {
-                float sums[CENTROIDS] = {0};
-                for (int i = 0; i < valid; ++i) sums[assign[i]] += x[i][d];
-                for (int s = 0; s < CENTROIDS; ++s) {
-                    const uint16_t c = counts[s] > 0 ? f32_to_bf16(sums[s] / (float)counts[s])
-                                                     : f32_to_bf16(0.0f);
-                    centroids[(row * CENTROIDS + s) * HEAD_DIM + d] =
-                        f32_to_bf16(bf16_to_f32(c) * qk_scale_log2);
-                }
+            if (slot + 1 < CENTROIDS) center = argmax_lowest(min_d, valid);
+        }
+        int counts[CENTROIDS] = {0};
+        for (int i = 0; i < valid; ++i) ++counts[assign[i]];
+        const int64_t row = bh * qb + blk;
+        for (int s = 0; s < CENTROIDS; ++s) pops[row * CENTROIDS + s] = (float)counts[s];
+        for (int d = 0; d < HEAD_DIM; ++d) {
+            float sums[CENTROIDS] = {0};
+            for (int i = 0; i < valid; ++i) sums[assign[i]] += x[i][d];
+            for (int s = 0; s < CENTROIDS; ++s) {
+                const uint16_t c = counts[s] > 0 ? f32_to_bf16(sums[s] / (float)counts[s])
+                                                 : f32_to_bf16(0.0f);
+                centroids[(row * CENTROIDS + s) * HEAD_DIM + d] =
+                    f32_to_bf16(bf16_to_f32(c) * qk_scale_log2);
             }
         }
     }
@@ -199,6 +215,7 @@ void orc_cluster(const uint16_t *q, int64_t bh_count, int64_t n, float qk_scale_
 /* k: bf16 [bh, n, 128] -> pooled bf16 [bh, n/4, 2, 128]. */
 void orc_pool(const uint16_t *k, int64_t bh_count, int64_t n, uint16_t *pooled) {
     const int64_t fb = n / KV_BLOCK;
+#pragma omp parallel for schedule(static)
     for (int64_t bh = 0; bh < bh_count; ++bh)
         for (int64_t j = 0; j < fb; ++j)
             for (int r = 0; r < REPS; ++r)
@@ -247,6 +264,7 @@ void orc_lse_rows(const uint16_t *centroids, int64_t rows, const uint16_t *poole
     float *rep = (float *)malloc(sizeof(float) * (size_t)fb * REPS * HEAD_DIM);
     if (!rep) return;
     for (int64_t i = 0; i < fb * REPS * HEAD_DIM; ++i) rep[i] = bf16_to_f32(pooled[i]);
+#pragma omp parallel for schedule(dynamic, 1)
     for (int64_t row = 0; row < rows; ++row) {
         for (int s = 0; s < CENTROIDS; ++s) {
             float c[HEAD_DIM];
@@ -298,6 +316,7 @@ void orc_lse(const uint16_t *centroids, const uint16_t *pooled, int64_t bh_count
 /* m_j = (sum_s fmaf(n_s, exp2f(l_sj - M_s) * (1/D_s), .)) * (1/sum_s n_s). */
 void orc_masses(const uint16_t *lse, const float *pops, const float *lse_max, const float *lse_den,
                 int64_t rows, int64_t fb, float *scores) {
+#pragma omp parallel for schedule(dynamic, 4)
     for (int64_t row = 0; row < rows; ++row) {
         float weight[CENTROIDS], inv_den[CENTROIDS], mx[CENTROIDS];
         float total = 0.0f;
@@ -393,6 +412,99 @@ static void block_exclusive_sum(const double *in, double *out) {
     }
 }
 
+/* One row of SIP: input [pop] masses, offset_f its uniform -> out/logs
+ * [samples]; values [pop] and prefix [buckets + 1] are scratch. */
+static void sip_row(const float *input, float offset_f, int pop, int64_t samples, int32_t *out, float *logs,
+                    float *values, double *prefix) {
+    const int buckets = (pop + SIP_BUCKET - 1) / SIP_BUCKET;
+    double part[SIP_THREADS], chunk_mass[SIP_THREADS], chunk_base[SIP_THREADS];
+    for (int i = 0; i < pop; ++i) values[i] = fmaxf(input[i], 1e-30f);
+    int certainty = 0;
+    double scale;
+    for (;;) { /* sip.cu:62-96 */
+        double maxima[SIP_THREADS];
+        for (int t = 0; t < SIP_THREADS; ++t) {
+            double s = 0.0, m = 0.0;
+            for (int i = t; i < pop; i += SIP_THREADS)
+                if (values[i] > 0.f) {
+                    const double v = fmax((double)values[i], 1e-30);
+                    s = s + v;
+                    m = fmax(m, v);
+                }
+            part[t] = s;
+            maxima[t] = m;
+        }
+        const double total = block_sum(part);
+        double maximum = 0.0;
+        for (int t = 0; t < SIP_THREADS; ++t) maximum = fmax(maximum, maxima[t]);
+        scale = (double)(samples - certainty) / total;
+        int added = 0;
+        if (maximum * scale >= 1.0) {
+            for (int i = 0; i < pop; ++i)
+                if (values[i] > 0.f && fmax((double)values[i], 1e-30) * scale >= 1.0) {
+                    values[i] = -values[i];
+                    ++added;
+                }
+        }
+        certainty += added;
+        if (added == 0) break;
+    }
+    const int chunk = ((buckets + SIP_THREADS - 1) / SIP_THREADS) * SIP_BUCKET; /* :99-101 */
+    int last = pop - 1;
+    while (last >= 0 && values[last] <= 0.f) --last;
+    if (certainty != 0) { /* :108-124: certain ids first, ascending, weight 0 */
+        int slot = 0;
+        for (int i = 0; i < pop; ++i)
+            if (values[i] < 0.f) {
+                out[slot] = i;
+                logs[slot++] = 0.f;
+            }
+    }
+    for (int t = 0; t < SIP_THREADS; ++t) { /* :126-128 */
+        const int begin = t * chunk;
+        const int end = begin + chunk < pop ? begin + chunk : pop;
+        double m = 0.0;
+        for (int i = begin; i < end; ++i) m = m + (values[i] > 0.f ? (double)values[i] * scale : 0.0);
+        chunk_mass[t] = m;
+    }
+    block_exclusive_sum(chunk_mass, chunk_base); /* :129-130 */
+    const int residuals = (int)samples - certainty;
+    prefix[buckets] = residuals;
+    for (int t = 0; t < SIP_THREADS; ++t) { /* :137-141 */
+        const int begin = t * chunk;
+        const int end = begin + chunk < pop ? begin + chunk : pop;
+        double cumulative = chunk_base[t];
+        for (int i = begin; i < end; ++i) {
+            if (i % SIP_BUCKET == 0) prefix[i / SIP_BUCKET] = i > last ? (double)residuals : cumulative;
+            cumulative = cumulative + (values[i] > 0.f ? (double)values[i] * scale : 0.0);
+        }
+    }
+    const double offset = (double)offset_f;
+    for (int slot = 0; slot < residuals; ++slot) { /* :144-166 */
+        const double threshold = offset + slot;
+        int lower = 0, upper = buckets;
+        while (lower < upper) {
+            const int middle = (lower + upper + 1) / 2;
+            if (prefix[middle] <= threshold)
+                lower = middle;
+            else
+                upper = middle - 1;
+        }
+        const int bucket = lower < buckets - 1 ? lower : buckets - 1;
+        double mass = prefix[bucket];
+        int selected = last;
+        const int stop = (bucket + 1) * SIP_BUCKET < pop ? (bucket + 1) * SIP_BUCKET : pop;
+        for (int i = bucket * SIP_BUCKET; i < stop; ++i) {
+            if (values[i] <= 0.f) continue;
+            selected = i;
+            mass = fma((double)values[i], scale, mass);
+            if (mass > threshold) break;
+        }
+        out[certainty + slot] = selected;
+        logs[certainty + slot] = (float)(-log2(fmax((double)input[selected], 1e-30) * scale));
+    }
+}
+
 /*
  * scores [rows, pop] f32, offsets [rows] f32 -> ids [rows, samples] int32 and
  * log2(1/pi) weights [rows, samples] f32. Returns 0, or 1 on bad sizes.
@@ -402,107 +514,25 @@ int orc_sip(const float *scores, const float *offsets, int64_t rows, int64_t pop
     if (population <= 0 || samples <= 0 || samples >= population) return 1;
     const int pop = (int)population;
     const int buckets = (pop + SIP_BUCKET - 1) / SIP_BUCKET;
-    float *values = malloc(sizeof(float) * (size_t)pop);
-    double *prefix = malloc(sizeof(double) * (size_t)(buckets + 1));
-    if (!values || !prefix) {
+    int failed = 0;
+#pragma omp parallel
+    {
+        float *values = malloc(sizeof(float) * (size_t)pop);
+        double *prefix = malloc(sizeof(double) * (size_t)(buckets + 1));
+#pragma omp for schedule(dynamic, 4)
+        for (int64_t row = 0; row < rows; ++row) {
+            if (!values || !prefix) {
+#pragma omp atomic write
+                failed = 1;
+                continue;
+            }
+            sip_row(scores + row * pop, offsets[row], pop, samples, ids + row * samples, weights + row * samples,
+                    values, prefix);
+        }
         free(values);
         free(prefix);
-        return 1;
     }
-    double part[SIP_THREADS], chunk_mass[SIP_THREADS], chunk_base[SIP_THREADS];
-    for (int64_t row = 0; row < rows; ++row) {
-        const float *input = scores + row * pop;
-        int32_t *out = ids + row * samples;
-        float *logs = weights + row * samples;
-        for (int i = 0; i < pop; ++i) values[i] = fmaxf(input[i], 1e-30f);
-        int certainty = 0;
-        double scale;
-        for (;;) { /* sip.cu:62-96 */
-            double maxima[SIP_THREADS];
-            for (int t = 0; t < SIP_THREADS; ++t) {
-                double s = 0.0, m = 0.0;
-                for (int i = t; i < pop; i += SIP_THREADS)
-                    if (values[i] > 0.f) {
-                        const double v = fmax((double)values[i], 1e-30);
-                        s = s + v;
-                        m = fmax(m, v);
-                    }
-                part[t] = s;
-                maxima[t] = m;
-            }
-            const double total = block_sum(part);
-            double maximum = 0.0;
-            for (int t = 0; t < SIP_THREADS; ++t) maximum = fmax(maximum, maxima[t]);
-            scale = (double)(samples - certainty) / total;
-            int added = 0;
-            if (maximum * scale >= 1.0) {
-                for (int i = 0; i < pop; ++i)
-                    if (values[i] > 0.f && fmax((double)values[i], 1e-30) * scale >= 1.0) {
-                        values[i] = -values[i];
-                        ++added;
-                    }
-            }
-            certainty += added;
-            if (added == 0) break;
-        }
-        const int chunk = ((buckets + SIP_THREADS - 1) / SIP_THREADS) * SIP_BUCKET; /* :99-101 */
-        int last = pop - 1;
-        while (last >= 0 && values[last] <= 0.f) --last;
-        if (certainty != 0) { /* :108-124: certain ids first, ascending, weight 0 */
-            int slot = 0;
-            for (int i = 0; i < pop; ++i)
-                if (values[i] < 0.f) {
-                    out[slot] = i;
-                    logs[slot++] = 0.f;
-                }
-        }
-        for (int t = 0; t < SIP_THREADS; ++t) { /* :126-128 */
-            const int begin = t * chunk;
-            const int end = begin + chunk < pop ? begin + chunk : pop;
-            double m = 0.0;
-            for (int i = begin; i < end; ++i) m = m + (values[i] > 0.f ? (double)values[i] * scale : 0.0);
-            chunk_mass[t] = m;
-        }
-        block_exclusive_sum(chunk_mass, chunk_base); /* :129-130 */
-        const int residuals = (int)samples - certainty;
-        prefix[buckets] = residuals;
-        for (int t = 0; t < SIP_THREADS; ++t) { /* :137-141 */
-            const int begin = t * chunk;
-            const int end = begin + chunk < pop ? begin + chunk : pop;
-            double cumulative = chunk_base[t];
-            for (int i = begin; i < end; ++i) {
-                if (i % SIP_BUCKET == 0) prefix[i / SIP_BUCKET] = i > last ? (double)residuals : cumulative;
-                cumulative = cumulative + (values[i] > 0.f ? (double)values[i] * scale : 0.0);
-            }
-        }
-        const double offset = (double)offsets[row];
-        for (int slot = 0; slot < residuals; ++slot) { /* :144-166 */
-            const double threshold = offset + slot;
-            int lower = 0, upper = buckets;
-            while (lower < upper) {
-                const int middle = (lower + upper + 1) / 2;
-                if (prefix[middle] <= threshold)
-                    lower = middle;
-                else
-                    upper = middle - 1;
-            }
-            const int bucket = lower < buckets - 1 ? lower : buckets - 1;
-            double mass = prefix[bucket];
-            int selected = last;
-            const int stop = (bucket + 1) * SIP_BUCKET < pop ? (bucket + 1) * SIP_BUCKET : pop;
-            for (int i = bucket * SIP_BUCKET; i < stop; ++i) {
-                if (values[i] <= 0.f) continue;
-                selected = i;
-                mass = fma((double)values[i], scale, mass);
-                if (mass > threshold) break;
-            }
-            out[certainty + slot] = selected;
-            logs[certainty + slot] = (float)(-log2(fmax((double)input[selected], 1e-30) * scale));
-        }
-    }
-    free(values);
-    free(prefix);
-    return 0;
+    return failed;
 }
 
 /* ---- weighted paged prefill (flashinfer_backend.py:30-59, :164-242) ---- */
@@ -524,58 +554,64 @@ int orc_prefill_kv(const float *q, const float *k, const float *v, int64_t bh_co
                    const int64_t *row_list, int64_t row_count, float *out, float *lse) {
     const int64_t qb = (n + QUERY_BLOCK - 1) / QUERY_BLOCK, fb = n_kv / KV_BLOCK;
     const int64_t keys = samples * KV_BLOCK;
-    double *logit = malloc(sizeof(double) * (size_t)keys);
-    if (!logit) return 1;
     const double scale = 1.0 / sqrt((double)HEAD_DIM);
     const double ln2 = log(2.0);
     const int64_t total_rows = bh_count * qb;
     const int64_t count = row_list ? row_count : total_rows;
     for (int64_t r = 0; r < count; ++r) {
         const int64_t row = row_list ? row_list[r] : r;
-        if (row < 0 || row >= total_rows) {
-            free(logit);
-            return 3;
-        }
-        const int64_t bh = row / qb, blk = row % qb;
-        {
+        if (row < 0 || row >= total_rows) return 3;
+        for (int64_t s = 0; s < samples; ++s)
+            if (ids[row * samples + s] < 0 || ids[row * samples + s] >= fb) return 2;
+    }
+    int failed = 0;
+#pragma omp parallel
+    {
+        double *logit = malloc(sizeof(double) * (size_t)keys);
+        /* one task per (row, query): rows of a short list still spread over the threads */
+#pragma omp for schedule(dynamic, 4)
+        for (int64_t task = 0; task < count * QUERY_BLOCK; ++task) {
+            const int64_t row = row_list ? row_list[task / QUERY_BLOCK] : task / QUERY_BLOCK;
+            const int64_t bh = row / qb, blk = row % qb;
+            const int64_t i = blk * QUERY_BLOCK + task % QUERY_BLOCK;
+            if (i >= n) continue;
+            if (!logit) {
+#pragma omp atomic write
+                failed = 1;
+                continue;
+            }
             const int32_t *rid = ids + row * samples;
             const float *rw = logw + row * samples;
-            for (int64_t i = blk * QUERY_BLOCK; i < n && i < (blk + 1) * QUERY_BLOCK; ++i) {
-                const float *qi = q + (bh * n + i) * HEAD_DIM;
-                double mx = -INFINITY;
-                for (int64_t s = 0; s < samples; ++s) {
-                    const int64_t j = rid[s];
-                    if (j < 0 || j >= fb) {
-                        free(logit);
-                        return 2;
-                    }
-                    for (int t = 0; t < KV_BLOCK; ++t) {
-                        const float *kt = k + (bh * n_kv + KV_BLOCK * j + t) * HEAD_DIM;
-                        double dot = 0.0;
-                        for (int d = 0; d < HEAD_DIM; ++d) dot += (double)qi[d] * (double)kt[d];
-                        const double z = dot * scale + (double)rw[s] * ln2;
-                        logit[s * KV_BLOCK + t] = z;
-                        if (z > mx) mx = z;
-                    }
+            const float *qi = q + (bh * n + i) * HEAD_DIM;
+            double mx = -INFINITY;
+            for (int64_t s = 0; s < samples; ++s) {
+                const int64_t j = rid[s];
+                for (int t = 0; t < KV_BLOCK; ++t) {
+                    const float *kt = k + (bh * n_kv + KV_BLOCK * j + t) * HEAD_DIM;
+                    double dot = 0.0;
+                    for (int d = 0; d < HEAD_DIM; ++d) dot += (double)qi[d] * (double)kt[d];
+                    const double z = dot * scale + (double)rw[s] * ln2;
+                    logit[s * KV_BLOCK + t] = z;
+                    if (z > mx) mx = z;
                 }
-                double acc[HEAD_DIM] = {0}, den = 0.0;
-                for (int64_t s = 0; s < samples; ++s) {
-                    const int64_t j = rid[s];
-                    for (int t = 0; t < KV_BLOCK; ++t) {
-                        const double p = exp(logit[s * KV_BLOCK + t] - mx);
-                        const float *vt = v + (bh * n_kv + KV_BLOCK * j + t) * HEAD_DIM;
-                        den += p;
-                        for (int d = 0; d < HEAD_DIM; ++d) acc[d] += p * (double)vt[d];
-                    }
-                }
-                float *oi = out + (bh * n + i) * HEAD_DIM;
-                for (int d = 0; d < HEAD_DIM; ++d) oi[d] = (float)(acc[d] / den);
-                if (lse) lse[bh * n + i] = (float)((mx + log(den)) / ln2);
             }
+            double acc[HEAD_DIM] = {0}, den = 0.0;
+            for (int64_t s = 0; s < samples; ++s) {
+                const int64_t j = rid[s];
+                for (int t = 0; t < KV_BLOCK; ++t) {
+                    const double p = exp(logit[s * KV_BLOCK + t] - mx);
+                    const float *vt = v + (bh * n_kv + KV_BLOCK * j + t) * HEAD_DIM;
+                    den += p;
+                    for (int d = 0; d < HEAD_DIM; ++d) acc[d] += p * (double)vt[d];
+                }
+            }
+            float *oi = out + (bh * n + i) * HEAD_DIM;
+            for (int d = 0; d < HEAD_DIM; ++d) oi[d] = (float)(acc[d] / den);
+            if (lse) lse[bh * n + i] = (float)((mx + log(den)) / ln2);
         }
+        free(logit);
     }
-    free(logit);
-    return 0;
+    return failed;
 }
 
 /* Q and K/V of the same length (the plan's case). */

@@ -84,8 +84,9 @@ def test_gpu_end_to_end_plan(oracle_mod, fx):
     """Parity protocol (4): the GPU's own plan (fused IBCS + SIP on the
     fixture's uniforms) into the GPU prefill, against the fp64 oracle prefill
     given that same plan (bf16 bar); the share of plan ids equal to the
-    oracle's own plan is reported (IBCS masses agree to ~1e-6, so it is
-    nearly 1, but it is not a parity gate)."""
+    oracle's own plan is gated at 0.99 (the IBCS masses agree to ~1e-6, so
+    it is 1.0 here; a draw moves only where that shifts a cumulative past a
+    threshold)."""
     from ab_attention import _C
     from ab_attention.flashinfer_backend import paged_attention
 
@@ -108,4 +109,4 @@ def test_gpu_end_to_end_plan(oracle_mod, fx):
     assert np.abs(lse.cpu().numpy().reshape(1, n) - want_lse).max() <= 1e-3
     match = float(np.mean(ids_g == fx["ids"]))
     print(f"end-to-end c0: plan ids equal to the oracle's own plan: {match:.4f}", flush=True)
-    assert match > 0.5
+    assert match >= 0.99, match

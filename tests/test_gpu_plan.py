@@ -70,17 +70,26 @@ def test_fused_plan_large_rows(n):
 def test_fused_plan_exact_probe_path():
     """With kept prefixes, a row whose thresholds could land in a rounding drop
     of the prefix array makes the reference's probes instead of the two-level
-    search; forcing that path for every row gives the same bits."""
+    search; ab_ibcs_sip_exact_draws takes that path for every row and must
+    give the same bits as ab_ibcs_sip and as _C.ibcs then _C.sip."""
     print("fused plan forced reference probes n=108000", flush=True)
     torch.manual_seed(9)
-    n = 108000
+    n, samples = 108000, 2048
     q, k = (torch.randn(1, 2, n, 128).to(torch.bfloat16).cuda() for _ in range(2))
+    ids_f, w_f, ids_s, w_s = _both(q, k, samples, seed=4)
+    _assert_same(ids_f, w_f, ids_s, w_s)
+    rows = ids_f.shape[0]
+    offsets = torch.rand(rows, generator=torch.Generator().manual_seed(4)).cuda()
+    ids_x = torch.empty_like(ids_f)
+    w_x = torch.empty_like(w_f)
     lib = _lib.load()
-    lib.ab_testing_force_exact_draws(1)
-    try:
-        _assert_same(*_both(q, k, 2048, seed=4))
-    finally:
-        lib.ab_testing_force_exact_draws(0)
+    ws_bytes = lib.ab_ibcs_sip_workspace_bytes(2, n)
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    _lib.check(lib.ab_ibcs_sip_exact_draws(_lib.ptr(q), _lib.ptr(k), None, 2, n, _lib.ptr(offsets), samples,
+                                           _lib.ptr(workspace), ws_bytes, _lib.ptr(ids_x), _lib.ptr(w_x),
+                                           _lib.stream(q.device)))
+    torch.cuda.synchronize()
+    _assert_same(ids_x, w_x, ids_s, w_s)
 
 
 def test_build_plan_uses_fused_path():

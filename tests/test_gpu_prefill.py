@@ -134,3 +134,38 @@ def test_prefill_workgroup_generations(oracle_mod):
     ids = np.sort(rng.choice(fb, size=(rows, samples), replace=True), axis=1).astype(np.int32)
     logw = (rng.random((rows, samples)) * 3).astype(np.float32)
     _check(q, k, v, ids, logw, oracle_mod)
+
+
+def test_prefill_neg_inf_blocks(oracle_mod):
+    """A -inf weight removes its block wherever it sits in the row: rows whose
+    first tile (8 blocks), first 20 blocks or a middle tile are at -inf match
+    the oracle over the remaining blocks; a row with every block at -inf
+    gives o = 0 and lse = -inf, not NaN."""
+    rng = np.random.default_rng(31)
+    torch.manual_seed(6)
+    n, samples = 1024, 64
+    rows, fb = n // 128, n // 4
+    q, k, v = (torch.randn(1, 1, n, 128).to(torch.bfloat16) for _ in range(3))
+    ids = np.sort(rng.choice(fb, size=(rows, samples), replace=True), axis=1).astype(np.int32)
+    logw = (rng.random((rows, samples)) * 3).astype(np.float32)
+    logw[0, :8] = -np.inf
+    logw[1, :20] = -np.inf
+    logw[2, 8:16] = -np.inf
+    logw[3, :] = -np.inf
+    logw[4, -8:] = -np.inf
+    print("prefill -inf blocks n=1024", flush=True)
+    desc = torch.from_numpy(ids.reshape(rows, 2, 32)).cuda()
+    w = torch.from_numpy(logw.reshape(rows, 2, 32)).cuda()
+    out, lse = paged_attention(q.cuda(), k.cuda(), v.cuda(), desc, w, return_lse=True)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy().reshape(n, 128)
+    got_lse = lse.cpu().numpy().reshape(n)
+    keep = np.array([0, 1, 2, 4, 5, 6, 7])
+    f32 = lambda t: t.float().numpy().reshape(1, n, 128)
+    ref_o, ref_lse = oracle_mod.prefill(f32(q), f32(k), f32(v), ids, logw, rows=keep)
+    for r in keep:
+        lo, hi = r * 128, r * 128 + 128
+        assert np.abs(got[lo:hi] - ref_o[0, lo:hi]).max() <= MAX_ABS, r
+        assert np.abs(got_lse[lo:hi] - ref_lse[0, lo:hi]).max() <= LSE_ABS, r
+    assert np.all(got[3 * 128:4 * 128] == 0.0)
+    assert np.all(np.isneginf(got_lse[3 * 128:4 * 128]))

@@ -117,3 +117,115 @@ def test_hunyuan_partition(oracle_mod, step, pad):
     _close(_f32(fused).reshape(2, n, 128), ref)
     _close(_f32(split).reshape(2, n, 128), ref)
     _close(_f32(fused), _f32(split))
+
+
+def test_dense_equals_listed_pages(oracle_mod):
+    """exact_attention walks the blocks with no page list (ab_dense_prefill);
+    the same kernel over an explicit list of every block at weight 0 (padded
+    to a multiple of 8 with -inf) gives the same bits, and a longer case is
+    within the bf16 bars of the oracle on its first and last rows."""
+    from ab_attention.paged import _prefill_kv
+    from ab_attention.video import _dense_pages
+
+    torch.manual_seed(17)
+    nq, nk = 4000, 4092
+    print(f"dense vs listed nq={nq} nk={nk}", flush=True)
+    q = torch.randn(1, 2, nq, 128).to(torch.bfloat16).cuda()
+    k = torch.randn(1, 2, nk, 128).to(torch.bfloat16).cuda()
+    v = torch.randn(1, 2, nk, 128).to(torch.bfloat16).cuda()
+    out, lse = exact_attention(q, k, v, return_lse=True)
+    rows = 2 * -(-nq // 128)
+    ids, w = _dense_pages(rows, nk // 4, q.device)
+    out_l, lse_l = _prefill_kv(q, k, v, ids, w, return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out_l)
+    assert torch.equal(lse, lse_l)
+    keep = np.array([0, rows // 2 - 1, rows // 2, rows - 1])
+    ids_o, w_o = _dense_plan(rows, nk // 4)
+    ref_o, ref_l = oracle_mod.prefill(_f32(q).reshape(2, nq, 128), _f32(k).reshape(2, nk, 128),
+                                      _f32(v).reshape(2, nk, 128), ids_o, w_o, rows=keep)
+    got, got_l = _f32(out).reshape(2, nq, 128), _f32(lse).reshape(2, nq)
+    for r in keep:
+        bh, blk = divmod(int(r), rows // 2)
+        lo, hi = blk * 128, min(nq, blk * 128 + 128)
+        _close(got[bh, lo:hi], ref_o[bh, lo:hi])
+        assert np.abs(got_l[bh, lo:hi] - ref_l[bh, lo:hi]).max() <= LSE_ABS
+
+
+def test_video_attention_plan_schedule(oracle_mod):
+    """The denoising schedule (reference: video.py:53-87): dense through step
+    10 and on layer 0; a layer's plan is built at anchor steps 11, 15, ...
+    with seed 42 + layer*1000003 + anchor*97, and reused in between, here
+    across steps 11, 12, 14 and 15 with new activations at every step. Each
+    plan equals build_plan with that seed; the rebuilt plan at step 15 is
+    bit-exact with the oracle's SIP on the GPU's scores and uniforms, and
+    every step's output is within the bf16 bars of the oracle given the plan
+    in use."""
+    from ab_attention import _C, apply_plan, build_plan
+
+    torch.manual_seed(23)
+    n, pages, layer = 2048, 2, 3
+    sched = VideoAttention(pages)
+    assert not sched.is_sparse(layer)
+    sched.step_end(None, 9, None, {})  # index 9 ends step 10; next is step 11
+    assert sched.step == 11 and sched.is_sparse(layer) and not sched.is_sparse(0)
+    plans = {}
+    for step in (11, 12, 14, 15):
+        sched.step = step
+        print(f"schedule step {step}", flush=True)
+        q, k, v = (torch.randn(1, 2, n, 128).to(torch.bfloat16).cuda() for _ in range(3))
+        out = sched.attend(layer, q, k, v)
+        anchor, plan = sched.plans[layer]
+        assert anchor == (11 if step < 15 else 15)
+        plans[step] = plan
+        seed = 42 + layer * 1_000_003 + anchor * 97
+        if step in (11, 15):
+            fresh = build_plan(q, k, sample_pages=pages, seed=seed)
+            assert torch.equal(fresh.descriptor, plan.descriptor)
+            assert torch.equal(fresh.log_weights.view(torch.int32), plan.log_weights.view(torch.int32))
+        else:
+            assert plan is plans[11]  # reused, not rebuilt
+        assert torch.equal(out, apply_plan(q, k, v, plan))
+        rows = plan.descriptor.shape[0]
+        ids = plan.descriptor.reshape(rows, -1).cpu().numpy()
+        w = plan.log_weights.reshape(rows, -1).cpu().numpy()
+        if step == 15:
+            offsets = torch.rand(rows, device=q.device, generator=torch.Generator(q.device).manual_seed(seed))
+            ids_o, w_o = oracle_mod.sip(_C.ibcs(q, k).cpu().numpy(), offsets.cpu().numpy(), pages * 32)
+            assert np.array_equal(ids, ids_o) and np.array_equal(w.view(np.uint32), w_o.view(np.uint32))
+        ref, _ = oracle_mod.prefill(*(_f32(t).reshape(2, n, 128) for t in (q, k, v)), ids, w)
+        _close(_f32(out).reshape(2, n, 128), ref)
+    assert plans[15] is not plans[11] and not torch.equal(plans[15].descriptor, plans[11].descriptor)
+
+
+def test_apply_plan_in_hip_graph():
+    """apply_plan recorded into a HIP graph (the reference runs its prefill
+    with CUDA-graph buffers, flashinfer_backend.py:132-143): every replay, with
+    new Q/K/V copied into the captured inputs and eager work and
+    synchronisations between replays, equals the eager call bit for bit."""
+    from ab_attention import apply_plan, build_plan
+
+    torch.manual_seed(29)
+    n, pages = 4096, 4
+    q, k, v = (torch.randn(1, 2, n, 128).to(torch.bfloat16).cuda() for _ in range(3))
+    plan = build_plan(q, k, sample_pages=pages, seed=5)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        apply_plan(q, k, v, plan, return_lse=True)  # warm-up outside capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_out, static_lse = apply_plan(q, k, v, plan, return_lse=True)
+    for i in range(4):
+        print(f"graph replay {i}", flush=True)
+        for t in (q, k, v):
+            t.copy_(torch.randn(t.shape, device=t.device).to(torch.bfloat16))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want, want_lse = apply_plan(q, k, v, plan, return_lse=True)
+        torch.cuda.synchronize()
+        assert torch.equal(static_out, want)
+        assert torch.equal(static_lse, want_lse)

@@ -49,6 +49,10 @@ def test_workspace_and_stride_queries():
     (lambda L: L.ab_ibcs(None, None, 1, 4 * 40000, None, 0, None, None), b"32768"),
     (lambda L: L.ab_paged_prefill(None, None, None, 1, 1024, None, None, 48, None, None, None), b"multiple of 32"),
     (lambda L: L.ab_paged_prefill(None, None, None, 1, 1024, None, None, 64, None, None, None), b"null pointer"),
+    (lambda L: L.ab_dense_prefill(None, None, None, 1, 1024, 1022, None, None, None), b"divisible by 4"),
+    (lambda L: L.ab_dense_prefill(None, None, None, 1, 1024, 1024, None, None, None), b"null pointer"),
+    (lambda L: L.ab_ibcs_sip_exact_draws(None, None, None, 1, 1024, None, 300, None, 0, None, None, None),
+     b"inside the population"),
 ])
 def test_validation_before_launch(call, msg):
     lib = _lib.load()
