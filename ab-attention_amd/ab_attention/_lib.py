@@ -41,6 +41,7 @@ SIGNATURES = {
     "ab_ibcs_sip": (ctypes.c_int, [_P, _P, _P, _I64, _I64, _P, _I64, _P, _SZ, _P, _P, _P]),
     "ab_ibcs_sip_exact_draws": (ctypes.c_int, [_P, _P, _P, _I64, _I64, _P, _I64, _P, _SZ, _P, _P, _P]),
     "ab_dense_prefill": (ctypes.c_int, [_P, _P, _P, _I64, _I64, _I64, _P, _P, _P]),
+    "ab_ibcs_sip_static": (ctypes.c_int, [_P, _P, _P, _I64, _I64, _P, _I64, _P, _P, _P]),
 }
 
 ABI_VERSION = 3

@@ -89,6 +89,22 @@ int ab_ibcs_sip(const void *q, const void *k, const int32_t *order, int64_t batc
                 const float *offsets, int64_t samples, void *workspace, size_t workspace_bytes, int32_t *ids,
                 float *log_weights, void *stream);
 
+/* ---- Fused plan without allocation ----------------------------------------
+ * No counterpart in the reference; for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). ab_ibcs_sip with the same arguments minus the workspace,
+ * giving the same bits. The IBCS intermediates live in a static device array
+ * of AB_STATIC_SCRATCH_BYTES that each GPU the library runs on holds until
+ * the process ends; heads run in chunks that fit it, and a shape whose single
+ * head needs more (tokens above 128,768) is rejected with AB_ERR_INVALID
+ * before any launch. The call allocates nothing (no hipMalloc, no hipFree).
+ * Calls that overlap on one GPU (other streams or threads) race on the
+ * array. The first call on a device resolves the array's address, a runtime
+ * call: make it outside graph capture. */
+#define AB_STATIC_SCRATCH_BYTES ((size_t)512 << 20)
+int ab_ibcs_sip_static(const void *q, const void *k, const int32_t *order, int64_t batch_heads, int64_t tokens,
+                       const float *offsets, int64_t samples, int32_t *ids, float *log_weights, void *stream);
+
 /* Testing variant of ab_ibcs_sip; no counterpart in the reference. Every
  * row that is sampled with kept prefixes takes the reference's binary-search
  * probes (each prefix rebuilt from the kept ones), the path otherwise taken

@@ -1,0 +1,71 @@
+"""ab_ibcs_sip_static, the fused plan without allocation (its IBCS
+intermediates live in a static device array of AB_STATIC_SCRATCH_BYTES per
+GPU), against ab_ibcs_sip with a caller workspace: ids and weights must be
+the same bits. Two calls in a row, the second smaller, so the second runs
+over what the first left in the shared array: 3 heads of the Wan2.1-14B
+720p length (two head chunks of the 512 MiB array), then 2 heads of 8,192
+tokens read through a token order. A head too long for the array is
+rejected before any launch."""
+import pytest
+import torch
+
+from ab_attention import _lib
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(heads, n, seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    q = torch.randn(1, heads, n, 128, device="cuda", generator=g).to(torch.bfloat16)
+    k = torch.randn(1, heads, n, 128, device="cuda", generator=g).to(torch.bfloat16)
+    rows = heads * -(-n // 128)
+    offsets = torch.rand(rows, device="cuda", generator=g)
+    return q, k, offsets
+
+
+def _with_workspace(lib, q, k, order, offsets, samples):
+    bh, n = q.shape[0] * q.shape[1], q.shape[2]
+    rows = offsets.shape[0]
+    ids = torch.empty(rows, samples, dtype=torch.int32, device="cuda")
+    w = torch.empty(rows, samples, dtype=torch.float32, device="cuda")
+    ws_bytes = lib.ab_ibcs_sip_workspace_bytes(bh, n)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    _lib.check(lib.ab_ibcs_sip(_lib.ptr(q), _lib.ptr(k), _lib.ptr(order), bh, n, _lib.ptr(offsets), samples,
+                               _lib.ptr(ws), ws_bytes, _lib.ptr(ids), _lib.ptr(w), _lib.stream(q.device)))
+    return ids, w
+
+
+def _static(lib, q, k, order, offsets, samples):
+    bh, n = q.shape[0] * q.shape[1], q.shape[2]
+    rows = offsets.shape[0]
+    ids = torch.full((rows, samples), -7, dtype=torch.int32, device="cuda")
+    w = torch.full((rows, samples), float("nan"), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    _lib.check(lib.ab_ibcs_sip_static(_lib.ptr(q), _lib.ptr(k), _lib.ptr(order), bh, n, _lib.ptr(offsets),
+                                      samples, _lib.ptr(ids), _lib.ptr(w), _lib.stream(q.device)))
+    return ids, w
+
+
+def test_static_plan_equals_workspace_plan():
+    lib = _lib.load()
+    for heads, n, samples, ordered, seed in ((3, 75600, 2048, False, 1), (2, 8192, 256, True, 2)):
+        print(f"static plan heads={heads} n={n} samples={samples} ordered={ordered}", flush=True)
+        q, k, offsets = _inputs(heads, n, seed)
+        order = (torch.randperm(n, generator=torch.Generator().manual_seed(seed)).to(torch.int32).cuda()
+                 if ordered else None)
+        ids_s, w_s = _static(lib, q, k, order, offsets, samples)
+        torch.cuda.synchronize()
+        ids_r, w_r = _with_workspace(lib, q, k, order, offsets, samples)
+        torch.cuda.synchronize()
+        assert torch.equal(ids_s, ids_r)
+        assert torch.equal(w_s.view(torch.int32), w_r.view(torch.int32))
+
+
+def test_static_plan_rejects_oversized_head():
+    lib = _lib.load()
+    n = 131072
+    q = torch.zeros(1, 1, 4096, 128, dtype=torch.bfloat16, device="cuda")  # never read: rejected first
+    rc = lib.ab_ibcs_sip_static(_lib.ptr(q), _lib.ptr(q), None, 1, n, _lib.ptr(q), 2048, _lib.ptr(q),
+                                _lib.ptr(q), _lib.stream(q.device))
+    assert rc == 1
+    assert b"static scratch" in lib.ab_last_error()
