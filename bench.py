@@ -6,17 +6,24 @@ B=2 (CFG pair), H=40, 75,600 tokens, d=128, 64 sample pages (8,192 keys per
 generated on the GPU and resident in HBM before timing starts.
 
 Reported (one JSON line on stdout):
-  value          effective TFLOP/s of the call = F_pre / call time, where
+  value          effective TFLOP/s of the call = F_pre / ms_per_step, where
                  F_pre = 4*d*(128*rows)*(4*S) is the prefill work done;
-  ms_per_step    ms per ab_attention call (mean over --steps);
-  roofline       the prefill kernel (the dominant one): F_pre / its mean
-                 duration (HIP events on the launch stream) vs the bf16 dense
-                 MFMA peak; traffic from the committed rocprofv3 counter runs
-                 (profiles/), or null;
-  selection      build_plan time and the reference-dataflow byte count B_sel
-                 divided by it, vs 8 TB/s;
-  cpu_baseline   the CPU oracle (one thread) on a bounded sample of rows of
-                 the same workload, extrapolated to a whole call.
+  ms_per_step    median over the --steps timed calls of the call's duration,
+                 HIP events on the launch stream (torch's current stream,
+                 which every launch of the library uses); wall_ms_per_step
+                 is the host clock over the same steps, synchronised on both
+                 sides, divided by --steps;
+  roofline       the prefill kernel (the dominant one): F_pre / its median
+                 duration (HIP events around the one launch) vs the bf16
+                 dense MFMA peak; traffic = HBM bytes per launch from the
+                 committed rocprofv3 counter runs (profiles/), or null;
+  selection      build_plan's median duration, and the reference-dataflow
+                 byte count B_sel divided by it, vs 8 TB/s;
+  dense          dense attention over the same Q/K/V (exact_attention: the
+                 reference's dense steps and layer 0), median of 3 calls,
+                 with its dense-equivalent work 4*d*N^2*B*H;
+  cpu_baseline   the CPU oracle on all host threads (OpenMP) over one whole
+                 head of the same workload, scaled by the head count.
 """
 from __future__ import annotations
 
@@ -24,6 +31,7 @@ import argparse
 import json
 import os
 import platform
+import statistics
 import sys
 import time
 
@@ -56,9 +64,21 @@ def _traffic_from_profiles():
         return json.load(f).get("traffic_bytes_per_launch")
 
 
-def cpu_baseline(q, k, v, cfg, sample_rows: int):
-    """Time the CPU oracle (single thread) on the first `sample_rows` query
-    blocks of head 0 and extrapolate to the full call's rows."""
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def cpu_baseline(q, k, v, cfg, head: int):
+    """Time the CPU oracle (IBCS, SIP and the fp64 weighted prefill, row loops
+    on every OpenMP thread) over all query blocks of one (batch 0, head) and
+    scale by the call's head count."""
     import numpy as np
     import torch
 
@@ -68,34 +88,25 @@ def cpu_baseline(q, k, v, cfg, sample_rows: int):
     n = cfg.tokens
     samples = cfg.sample_pages * 32
     bits = lambda t: np.ascontiguousarray(t.contiguous().view(torch.int16).numpy().view(np.uint16))
-    q0 = q[0, 0].cpu()
-    k0 = k[0, 0].cpu()
-    v0 = v[0, 0].cpu()
-    toks = sample_rows * 128
+    q0, k0, v0 = (t[0, head].cpu() for t in (q, k, v))
+    qb = -(-n // 128)
+    offsets = np.random.default_rng(0).random(qb).astype(np.float32)
+    qf, kf, vf = (t.float().numpy()[None] for t in (q0, k0, v0))
     t0 = time.perf_counter()
-    cent, pops = oracle.cluster(bits(q0[:toks]).reshape(1, toks, 128), 1, toks)
-    pooled = oracle.pool(bits(k0).reshape(1, n, 128), 1, n)
-    lse, mx, den = oracle.lse_rows(cent, pooled[0])
-    scores = oracle.masses(lse, pops, mx, den, sample_rows, n // 4)
-    offsets = np.random.default_rng(0).random(sample_rows).astype(np.float32)
+    scores = oracle.ibcs(bits(q0).reshape(1, n, 128), bits(k0).reshape(1, n, 128), 1, n)
     ids, logw = oracle.sip(scores, offsets, samples)
-    qf = np.zeros((1, n, 128), np.float32)
-    qf[0, :toks] = q0[:toks].float().numpy()
-    full_ids = np.zeros((-(-n // 128), samples), np.int32)
-    full_w = np.zeros_like(full_ids, dtype=np.float32)
-    full_ids[:sample_rows], full_w[:sample_rows] = ids, logw
-    oracle.prefill(qf, k0.float().numpy()[None], v0.float().numpy()[None], full_ids, full_w,
-                   rows=np.arange(sample_rows))
+    oracle.prefill(qf, kf, vf, ids, logw)
     elapsed = time.perf_counter() - t0
-    total_rows = cfg.batch * cfg.heads * -(-n // 128)
+    heads = cfg.batch * cfg.heads
     return {
-        "value": round(elapsed / sample_rows * total_rows * 1e3, 1),
-        "unit": "ms per AB-attn call (extrapolated)",
-        "cores": 1,
+        "value": round(elapsed * heads * 1e3, 1),
+        "unit": "ms per AB-attn call (one head timed, scaled by B*H)",
+        "cores": oracle.num_threads(),
         "kind": "port",
-        "sample": (f"{sample_rows} query blocks of head 0 (IBCS + SIP + weighted prefill, oracle C, fp64 "
-                   f"prefill) in {elapsed:.1f} s, scaled by {total_rows} rows"),
-        "cpu": platform.processor() or platform.machine(),
+        "sample": (f"all {qb} query blocks of one head (batch 0, head {head}): IBCS + SIP + weighted "
+                   f"prefill (oracle C, fp64 prefill) in {elapsed:.1f} s on {oracle.num_threads()} threads, "
+                   f"scaled by {heads} heads"),
+        "cpu": _cpu_model(),
     }
 
 
@@ -106,9 +117,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=2, help="BASELINE config index (default 2)")
     ap.add_argument("--heads", type=int, default=None, help="override head count (profiling only)")
-    ap.add_argument("--cpu-sample-rows", type=int, default=80,
-                    help="query blocks of head 0 timed on the CPU oracle (about 10 s on the GPU box host)")
+    ap.add_argument("--cpu-head", type=int, default=0,
+                    help="head (of batch item 0) timed on the CPU oracle, all its query blocks")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-dense", action="store_true", help="skip the dense-attention timing")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy (HBM counter calibration)")
     args = ap.parse_args()
@@ -160,6 +172,8 @@ def main() -> int:
             return (_remap_ids(plan.descriptor.reshape(rows, samples), page_map),
                     plan.log_weights.reshape(rows, samples), order)
 
+    stream = torch.cuda.current_stream()
+
     def step():
         plan = build_plan(q, k, sample_pages=cfg.sample_pages, seed=42)
         return apply_plan(q, k, v, plan)
@@ -167,33 +181,38 @@ def main() -> int:
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    # The timed region: exactly --steps calls, synchronised on both sides,
+    # with a HIP event pair around each call on the launch stream.
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for start, stop in ev:
+        start.record(stream)
         step()
+        stop.record(stream)
     torch.cuda.synchronize()
-    ms_call = (time.perf_counter() - t0) * 1e3 / args.steps
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    ms_call = statistics.median(a.elapsed_time(b) for a, b in ev)
 
-    # Breakdown with HIP events on the launch stream (torch's current stream,
-    # which every launch of the library uses): build_plan (selection) and the
-    # prefill kernel alone (one launch).
+    # Breakdown with HIP events on the launch stream: build_plan (selection)
+    # and the prefill kernel alone (one launch, recorded while build_plan's
+    # kernels still run, so no host gap is timed).
     from ab_attention.paged import _prefill
 
-    stream = torch.cuda.current_stream()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
     sel_ms, pre_ms = [], []
     for _ in range(max(3, args.steps)):
-        ev[0].record(stream)
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        e[0].record(stream)
         plan = build_plan(q, k, sample_pages=cfg.sample_pages, seed=42)
-        ev[1].record(stream)
+        e[1].record(stream)
         ids, weights, order = prefill_inputs(plan)
-        ev[2].record(stream)
+        e[2].record(stream)
         _prefill(q, k, v, ids, weights, order, False)
-        ev[3].record(stream)
+        e[3].record(stream)
         torch.cuda.synchronize()
-        sel_ms.append(ev[0].elapsed_time(ev[1]))
-        pre_ms.append(ev[2].elapsed_time(ev[3]))
-    sel = sum(sel_ms) / len(sel_ms)
-    pre = sum(pre_ms) / len(pre_ms)
+        sel_ms.append(e[0].elapsed_time(e[1]))
+        pre_ms.append(e[2].elapsed_time(e[3]))
+    sel = statistics.median(sel_ms)
+    pre = statistics.median(pre_ms)
 
     achieved = f_pre / (pre * 1e-3) / 1e12
     result = {
@@ -204,6 +223,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_call, 3),
+        "wall_ms_per_step": round(wall_ms, 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -219,10 +239,29 @@ def main() -> int:
         "selection": {"ms": round(sel, 3), "bytes_gb": round(b_sel / 1e9, 3),
                       "effective_gbs": round(b_sel / (sel * 1e-3) / 1e9, 1),
                       "frac_of_hbm": round(b_sel / (sel * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
+        "dense": None,
         "cpu_baseline": None,
     }
+    if not args.no_dense and not cfg.text_tokens:
+        from ab_attention.video import exact_attention
+
+        exact_attention(q, k, v)
+        dense_ms = []
+        for _ in range(3):
+            e = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+            e[0].record(stream)
+            exact_attention(q, k, v)
+            e[1].record(stream)
+            torch.cuda.synchronize()
+            dense_ms.append(e[0].elapsed_time(e[1]))
+        dms = statistics.median(dense_ms)
+        f_dense = 4.0 * 128 * n * n * bh
+        result["dense"] = {"ms": round(dms, 3), "work_tflop": round(f_dense / 1e12, 3),
+                           "tflops": round(f_dense / (dms * 1e-3) / 1e12, 1),
+                           "frac": round(f_dense / (dms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                           "kernel": "prefill_kernel<dense>"}
     if not args.no_cpu_baseline and args.heads is None:
-        result["cpu_baseline"] = cpu_baseline(q, k, v, cfg, args.cpu_sample_rows)
+        result["cpu_baseline"] = cpu_baseline(q, k, v, cfg, args.cpu_head)
     print(json.dumps(result), flush=True)
     return 0
 
