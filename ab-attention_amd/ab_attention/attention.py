@@ -5,19 +5,26 @@ Same public surface as the reference's ``ab_attention/attention.py``:
 same arguments, defaults, validation (ValueError) and plan layout.
 
 Differences that do not change results:
-  - the IBCS scratch budget per head chunk is sized for 288 GB of HBM, so the
-    Wan2.1-14B 720p call runs as one chunk instead of nine; rows are
-    independent and the offsets are drawn before chunking, so the plan does
-    not depend on the chunking (attention.py:54-75 in the reference);
+  - the IBCS scratch budget per head chunk (``LSE_BUDGET_BYTES``) defaults
+    to 16 GiB, sized for 288 GB of HBM, so the Wan2.1-14B 720p call runs as
+    one chunk instead of nine; rows are independent and the offsets are
+    drawn before chunking, so the plan does not depend on the chunking
+    (attention.py:54-75 in the reference). A caller that shares the GPU can
+    lower it: set ``ab_attention.attention.LSE_BUDGET_BYTES`` or the
+    environment variable ``AB_ATTENTION_LSE_BUDGET_BYTES`` (read at import);
+    the reference's value is 1.5 GiB;
   - ``apply_plan`` goes to the gfx950 paged prefill in ``paged.py``.
 """
 import math
+import os
 from typing import NamedTuple
 
 import torch
 
-# IBCS keeps [rows, 8, ~tokens/4] fp16 pair-LSEs per head chunk.
-_LSE_BUDGET_BYTES = 16 * 1024 * 1024 * 1024
+# Budget for the [rows, 8, ~tokens/4] fp16 pair-LSEs of one head chunk; the
+# whole IBCS workspace of a chunk is about 1.07 times this (plus pooled keys
+# and centroids). At least one head is processed per chunk.
+LSE_BUDGET_BYTES = int(os.environ.get("AB_ATTENTION_LSE_BUDGET_BYTES", 16 * 1024 ** 3))
 
 
 class SamplePlan(NamedTuple):
@@ -38,7 +45,7 @@ class SamplePlan(NamedTuple):
 
 def _heads_per_chunk(batch_heads: int, q_blocks: int, tokens: int) -> int:
     lse_bytes_per_head = q_blocks * 8 * (tokens // 4) * 2
-    return max(1, min(batch_heads, _LSE_BUDGET_BYTES // lse_bytes_per_head))
+    return max(1, min(batch_heads, int(LSE_BUDGET_BYTES) // lse_bytes_per_head))
 
 
 @torch.no_grad()

@@ -121,6 +121,8 @@ def main() -> int:
                     help="head (of batch item 0) timed on the CPU oracle, all its query blocks")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-dense", action="store_true", help="skip the dense-attention timing")
+    ap.add_argument("--lse-budget-gib", type=float, default=None,
+                    help="IBCS head-chunk budget (default: the library's 16 GiB; the reference uses 1.5)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy (HBM counter calibration)")
     args = ap.parse_args()
@@ -143,6 +145,10 @@ def main() -> int:
     from ab_attention import apply_plan, build_plan
     from ab_attention.synthetic import CONFIGS, make_qkv
 
+    if args.lse_budget_gib is not None:
+        from ab_attention import attention
+
+        attention.LSE_BUDGET_BYTES = int(args.lse_budget_gib * 1024 ** 3)
     cfg = CONFIGS[args.config]
     heads = None if args.heads is None else list(range(args.heads))
     dev = torch.device("cuda", 0)

@@ -115,3 +115,18 @@ def test_video_validation_errors():
     sched.step = 11
     assert sched.is_sparse(1) and not sched.is_sparse(0)
     assert not VideoAttention(4, dense=True).is_sparse(3)
+
+
+def test_lse_budget_sets_head_chunks(monkeypatch):
+    """LSE_BUDGET_BYTES bounds the pair-LSE bytes of one head chunk (at least
+    one head per chunk); the reference's 1.5 GiB gives its nine chunks of at
+    most 9 heads at Wan2.1-14B 720p (attention.py:8, :61-64)."""
+    from ab_attention import attention
+
+    per_head = 591 * 8 * 18900 * 2
+    monkeypatch.setattr(attention, "LSE_BUDGET_BYTES", int(1.5 * 1024 ** 3))
+    assert attention._heads_per_chunk(80, 591, 75600) == 9
+    monkeypatch.setattr(attention, "LSE_BUDGET_BYTES", per_head - 1)
+    assert attention._heads_per_chunk(80, 591, 75600) == 1
+    monkeypatch.setattr(attention, "LSE_BUDGET_BYTES", 16 * 1024 ** 3)
+    assert attention._heads_per_chunk(80, 591, 75600) == 80

@@ -105,3 +105,18 @@ def test_build_plan_uses_fused_path():
     _C.sip(_C.ibcs(q, k), offsets, ids, w)
     torch.cuda.synchronize()
     _assert_same(plan.descriptor.reshape(rows, 64), plan.log_weights.reshape(rows, 64), ids, w)
+
+
+def test_build_plan_independent_of_head_chunks(monkeypatch):
+    """Lowering the IBCS budget to one head per chunk (one native call per
+    head) leaves the plan bit-identical: the uniforms are drawn first."""
+    from ab_attention import attention
+
+    print("build_plan chunking", flush=True)
+    torch.manual_seed(12)
+    q, k = (torch.randn(2, 3, 4096, 128).to(torch.bfloat16).cuda() for _ in range(2))
+    whole = build_plan(q, k, sample_pages=4, seed=3)
+    monkeypatch.setattr(attention, "LSE_BUDGET_BYTES", 1)
+    chunked = build_plan(q, k, sample_pages=4, seed=3)
+    torch.cuda.synchronize()
+    _assert_same(whole.descriptor, whole.log_weights, chunked.descriptor, chunked.log_weights)
