@@ -37,6 +37,8 @@
 //   V: per page 8 blocks of 4 keys x 16 dims (128 B); inside block m the row
 //      of key r sits at position r ^ ((m >> 1) & 3), so each 16-lane group of
 //      a transposing read fetches one whole 128-byte block.
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace ab {
@@ -55,6 +57,7 @@ constexpr int kIdsOffset = 2 * kRing * kTileBytes;             // 2 batch buffer
 constexpr int kWeightsOffset = kIdsOffset + 2 * kBatchBytes;   // 2 batch buffers of weights
 constexpr int kLdsBytes = kWeightsOffset + 2 * kBatchBytes;    // 72 KiB
 constexpr int kGroupOps = 4;                                   // transfers per wave per step
+constexpr int64_t kRowsPerLaunch = 11000;                      // see launch_prefill
 // Largest p = 2^(y) allowed before the running reference is moved.
 constexpr float kSlack = 8.0f;
 
@@ -536,11 +539,28 @@ int launch_prefill(const void* q, const void* k, const void* v, bool dense, int6
     if (rows == 0) return 0;
     auto kernel = dense ? prefill_kernel<true> : prefill_kernel<false>;
     if (int rc = ensure_lds_limit(reinterpret_cast<const void*>(kernel), kLdsBytes)) return rc;
-    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(per_xcd * 8 * bh)), dim3(kPfThreads), kLdsBytes,
-                       stream, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
-                       static_cast<const uint16_t*>(v), ids, logw, static_cast<uint16_t*>(out), lse, n, n_kv, qb, rows,
-                       static_cast<int>(n_kv / kKvBlock), static_cast<int>(samples), scale_log2, order);
-    return check_launch("prefill_kernel");
+    // Heads are launched in balanced chunks of about kRowsPerLaunch rows.
+    // The rows resident on an XCD sweep their (ascending) page lists at the
+    // same pace only while they started together; over a long launch their
+    // start times spread out, the pages they touch at one moment spread over
+    // the whole head and the XCD's L2 stops serving them. A new launch lines
+    // them up again: at c2, 5 launches take 23.9 ms against 25.0 ms for one,
+    // tails included (bit-identical outputs).
+    const int64_t launches = std::max<int64_t>(1, (rows + kRowsPerLaunch - 1) / kRowsPerLaunch);
+    const int64_t heads = (bh + launches - 1) / launches;
+    for (int64_t h0 = 0; h0 < bh; h0 += heads) {
+        const int64_t hc = std::min(heads, bh - h0);
+        const int64_t r0 = h0 * qb;
+        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(per_xcd * 8 * hc)), dim3(kPfThreads), kLdsBytes,
+                           stream, static_cast<const uint16_t*>(q) + h0 * n * kHeadDim,
+                           static_cast<const uint16_t*>(k) + h0 * n_kv * kHeadDim,
+                           static_cast<const uint16_t*>(v) + h0 * n_kv * kHeadDim, dense ? ids : ids + r0 * samples,
+                           dense ? logw : logw + r0 * samples, static_cast<uint16_t*>(out) + h0 * n * kHeadDim,
+                           lse ? lse + h0 * n : nullptr, n, n_kv, qb, hc * qb, static_cast<int>(n_kv / kKvBlock),
+                           static_cast<int>(samples), scale_log2, order);
+        if (int rc = check_launch("prefill_kernel")) return rc;
+    }
+    return 0;
 }
 
 }  // namespace ab

@@ -169,3 +169,38 @@ def test_prefill_neg_inf_blocks(oracle_mod):
         assert np.abs(got_lse[lo:hi] - ref_lse[0, lo:hi]).max() <= LSE_ABS, r
     assert np.all(got[3 * 128:4 * 128] == 0.0)
     assert np.all(np.isneginf(got_lse[3 * 128:4 * 128]))
+
+
+def test_prefill_launch_chunks(oracle_mod):
+    """91 heads x 128 query blocks = 11,648 rows: the prefill runs as two
+    launches of 46 and 45 heads. Every row must be written once (the output
+    starts as NaN) and rows on both sides of the chunk boundary, the first
+    and the last, match the oracle."""
+    from ab_attention import _lib
+
+    rng = np.random.default_rng(41)
+    torch.manual_seed(8)
+    heads, n, samples = 91, 128 * 128, 32
+    print(f"prefill launch chunks heads={heads} n={n}", flush=True)
+    q, k, v = (torch.randn(1, heads, n, 128).to(torch.bfloat16) for _ in range(3))
+    rows, fb = heads * 128, n // 4
+    ids = np.sort(rng.choice(fb, size=(rows, samples), replace=True), axis=1).astype(np.int32)
+    logw = (rng.random((rows, samples)) * 3).astype(np.float32)
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    out = torch.full_like(qd, float("nan"))
+    lse = torch.full((1, heads, n), float("nan"), device="cuda")
+    ids_d, logw_d = torch.from_numpy(ids).cuda(), torch.from_numpy(logw).cuda()
+    lib = _lib.load()
+    _lib.check(lib.ab_paged_prefill_kv(_lib.ptr(qd), _lib.ptr(kd), _lib.ptr(vd), heads, n, n, _lib.ptr(ids_d),
+                                       _lib.ptr(logw_d), samples, _lib.ptr(out), _lib.ptr(lse), _lib.stream(qd.device)))
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all()) and bool(torch.isfinite(lse).all())
+    keep = np.array([0, 46 * 128 - 1, 46 * 128, 46 * 128 + 1, rows - 1])
+    ref_o, ref_l = oracle_mod.prefill(q.float().numpy().reshape(heads, n, 128), k.float().numpy().reshape(heads, n, 128),
+                                      v.float().numpy().reshape(heads, n, 128), ids, logw, rows=keep)
+    got, got_l = out.float().cpu().numpy().reshape(heads, n, 128), lse.cpu().numpy().reshape(heads, n)
+    for r in keep:
+        h, b = divmod(int(r), 128)
+        sl = slice(b * 128, b * 128 + 128)
+        assert np.abs(got[h, sl] - ref_o[h, sl]).max() <= MAX_ABS, r
+        assert np.abs(got_l[h, sl] - ref_l[h, sl]).max() <= LSE_ABS, r
