@@ -13,7 +13,8 @@ in cube order, so the kernels need nothing special for it.
 (FA3 dense prefill with base-2 LSE, video.py:13-28) and ``_merge``
 (FlashInfer merge_state, video.py:31-40); both run on this library's kernels.
 ``VideoAttention`` is the reference's denoising schedule (video.py:53-87) with
-the plans kept on the GPU. ``hunyuan_attention`` is ``_hunyuan_attention``
+the plans kept on the GPU, or in pinned host memory (``offload=True``) as the
+reference keeps them. ``hunyuan_attention`` is ``_hunyuan_attention``
 (video.py:129-151): by default the video queries attend to their sampled pages
 and to every text block (weight 0) in one prefill, which equals the
 reference's sampled state merged with the exact text state.
@@ -190,16 +191,32 @@ def merge_states(state_a, state_b, *, return_lse: bool = False):
     return (out, lse) if return_lse else out
 
 
+def _store_plan(plan: SamplePlan, previous) -> SamplePlan:
+    """Copy a plan into pinned host memory, reusing the previous buffers
+    (reference: _store_plan, video.py:43-50)."""
+    if previous is None or previous.descriptor.shape != plan.descriptor.shape:
+        previous = SamplePlan(*(torch.empty(t.shape, dtype=t.dtype, pin_memory=True) for t in plan))
+    for storage, tensor in zip(previous, plan):
+        storage.copy_(tensor)
+    return previous
+
+
 class VideoAttention:
     """One pipeline's denoising schedule and per-layer sample plans
     (reference: video.py:53-87). Steps 1-10 and layer 0 stay dense; other
-    layers build a plan on steps 11, 15, ..., and reuse it in between. The
-    plans stay on the GPU (the reference parks them in pinned host memory).
+    layers build a plan on steps 11, 15, ..., and reuse it in between.
+
+    By default the plans stay on the GPU (two [rows, pages, 32] tensors per
+    layer: 774 MB per layer at Wan2.1-14B 720p with B=2, which 288 GB of
+    HBM holds for every layer). With ``offload=True`` they are kept in
+    pinned host memory and copied back on each reuse, as the reference does
+    for GPUs that cannot hold them.
     """
 
-    def __init__(self, sample_pages: int, *, dense: bool = False):
+    def __init__(self, sample_pages: int, *, dense: bool = False, offload: bool = False):
         self.sample_pages = sample_pages
         self.dense = dense
+        self.offload = offload
         self.reset()
 
     def reset(self):
@@ -218,10 +235,14 @@ class VideoAttention:
         (seed 42 + layer*1000003 + anchor*97, as the reference), else reused."""
         anchor = 11 + (self.step - 11) // 4 * 4
         stored_anchor, stored = self.plans.get(layer, (None, None))
-        if stored_anchor != anchor or stored.descriptor.device != q.device:
+        stale = stored_anchor != anchor or (not self.offload and stored.descriptor.device != q.device)
+        if stale:
             seed = 42 + layer * 1_000_003 + anchor * 97
-            stored = build_plan(q, k, sample_pages=self.sample_pages, seed=seed)
-            self.plans[layer] = (anchor, stored)
+            plan = build_plan(q, k, sample_pages=self.sample_pages, seed=seed)
+            self.plans[layer] = (anchor, _store_plan(plan, stored) if self.offload else plan)
+            return plan
+        if self.offload:
+            return SamplePlan(*(t.to(q.device, non_blocking=True) for t in stored))
         return stored
 
     def attend(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, return_lse: bool = False):

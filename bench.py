@@ -14,9 +14,12 @@ Reported (one JSON line on stdout):
                  is the host clock over the same steps, synchronised on both
                  sides, divided by --steps;
   roofline       the prefill kernel (the dominant one): F_pre / its median
-                 duration (HIP events around the one launch) vs the bf16
-                 dense MFMA peak; traffic = HBM bytes per launch from the
-                 committed rocprofv3 counter runs (profiles/), or null;
+                 duration (HIP events around its launches: the heads of a
+                 call are launched in balanced chunks of ~11,000 rows, 5 at
+                 c2, so this equals the per-launch work over the mean launch
+                 duration) vs the bf16 dense MFMA peak; traffic = HBM bytes
+                 per launch from the committed rocprofv3 counter runs
+                 (profiles/), or null;
   selection      build_plan's median duration, and the reference-dataflow
                  byte count B_sel divided by it, vs 8 TB/s;
   dense          dense attention over the same Q/K/V (exact_attention: the
@@ -55,10 +58,19 @@ def work_figures(bh: int, n: int, samples: int):
     return rows, fb, f_pre, b_sel
 
 
-def _traffic_from_profiles():
-    """HBM bytes per prefill launch from the committed counter summary, if any."""
+# Rows per prefill launch: the library launches the heads of a call in
+# balanced chunks of about this many rows (kRowsPerLaunch, csrc/prefill.hip).
+ROWS_PER_PREFILL_LAUNCH = 11000
+
+
+def prefill_launches(bh: int, qb: int) -> int:
+    return max(1, -(-bh * qb // ROWS_PER_PREFILL_LAUNCH))
+
+
+def _traffic_from_profiles(workload: str):
+    """HBM bytes per prefill launch from the committed counter summary (c2 only)."""
     path = os.path.join(ROOT, "profiles", "prefill_traffic_c2.json")
-    if not os.path.exists(path):
+    if not os.path.exists(path) or workload != "wan2.1-14b-720p":
         return None
     with open(path) as f:
         return json.load(f).get("traffic_bytes_per_launch")
@@ -220,6 +232,10 @@ def main() -> int:
     sel = statistics.median(sel_ms)
     pre = statistics.median(pre_ms)
 
+    # Per launch: the launches are balanced (equal head counts, the last may
+    # be smaller), so F_pre / launches over the mean launch duration equals
+    # F_pre over the prefill's total duration.
+    launches = prefill_launches(bh, -(-n // 128))
     achieved = f_pre / (pre * 1e-3) / 1e12
     result = {
         "metric": METRIC,
@@ -240,8 +256,10 @@ def main() -> int:
                    "rows": rows, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": _traffic_from_profiles(), "kernel": "prefill_kernel",
-                     "ms": round(pre, 3), "work_tflop": round(f_pre / 1e12, 3)},
+                     "traffic": _traffic_from_profiles(cfg.name), "kernel": "prefill_kernel",
+                     "launches": launches, "ms": round(pre, 3), "ms_per_launch": round(pre / launches, 3),
+                     "work_tflop": round(f_pre / 1e12, 3),
+                     "work_tflop_per_launch": round(f_pre / launches / 1e12, 3)},
         "selection": {"ms": round(sel, 3), "bytes_gb": round(b_sel / 1e9, 3),
                       "effective_gbs": round(b_sel / (sel * 1e-3) / 1e9, 1),
                       "frac_of_hbm": round(b_sel / (sel * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
