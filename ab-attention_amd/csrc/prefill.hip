@@ -105,7 +105,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const int32_t* __restrict__ ids, const float* __restrict__ logw, uint16_t* __restrict__ out,
     float* __restrict__ lse, int64_t n, int64_t n_kv, int64_t qb, int64_t rows, int fb, int samples,
-    float scale_log2, const int32_t* __restrict__ order) {
+    float scale_log2, const int32_t* __restrict__ order, int64_t slot_base) {
     extern __shared__ __align__(16) unsigned char smem[];
 
     // XCD-aware row order. The hardware deals workgroups round-robin over the
@@ -116,9 +116,10 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
     // Within an XCD, slots s and s + 32 of each full generation of 64 slots
     // run on the same CU (two workgroups per CU), so they take adjacent
     // query blocks: their sampled pages overlap and they sweep them in step,
-    // which turns part of the gathers into L1 hits.
+    // which turns part of the gathers into L1 hits. A launch covers the
+    // slots from slot_base (a multiple of 64) on, on every XCD.
     const int64_t hw = blockIdx.x;
-    const int64_t xcd = hw & 7, slot0 = hw >> 3;
+    const int64_t xcd = hw & 7, slot0 = slot_base + (hw >> 3);
     const int64_t per_xcd = (qb + 7) / 8;
     const int64_t generation = slot0 >> 6, s64 = slot0 & 63;
     const int64_t slot = (generation + 1) * 64 <= per_xcd * (rows / qb)
@@ -539,25 +540,27 @@ int launch_prefill(const void* q, const void* k, const void* v, bool dense, int6
     if (rows == 0) return 0;
     auto kernel = dense ? prefill_kernel<true> : prefill_kernel<false>;
     if (int rc = ensure_lds_limit(reinterpret_cast<const void*>(kernel), kLdsBytes)) return rc;
-    // Heads are launched in balanced chunks of about kRowsPerLaunch rows.
-    // The rows resident on an XCD sweep their (ascending) page lists at the
-    // same pace only while they started together; over a long launch their
-    // start times spread out, the pages they touch at one moment spread over
-    // the whole head and the XCD's L2 stops serving them. A new launch lines
-    // them up again: at c2, 5 launches take 23.9 ms against 25.0 ms for one,
-    // tails included (bit-identical outputs).
+    // The rows are launched in chunks of about kRowsPerLaunch, each a whole
+    // number of generations (64 row slots per XCD; a generation is what the
+    // chip holds at once, two workgroups per CU). The rows resident on an XCD
+    // sweep their (ascending) page lists at the same pace only while they
+    // started together; over a long launch their start times spread out, the
+    // pages they touch at one moment spread over the whole head and the XCD's
+    // L2 stops serving them. A new launch lines them up again (at c2, one
+    // launch: 25.0 ms; five launches of whole heads: 23.9 ms, bit-identical),
+    // and whole generations leave no half-empty generation in each launch.
+    const int64_t slots = per_xcd * bh;                    // row slots per XCD
+    const int64_t generations = (slots + 63) / 64;
     const int64_t launches = std::max<int64_t>(1, (rows + kRowsPerLaunch - 1) / kRowsPerLaunch);
-    const int64_t heads = (bh + launches - 1) / launches;
-    for (int64_t h0 = 0; h0 < bh; h0 += heads) {
-        const int64_t hc = std::min(heads, bh - h0);
-        const int64_t r0 = h0 * qb;
-        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(per_xcd * 8 * hc)), dim3(kPfThreads), kLdsBytes,
-                           stream, static_cast<const uint16_t*>(q) + h0 * n * kHeadDim,
-                           static_cast<const uint16_t*>(k) + h0 * n_kv * kHeadDim,
-                           static_cast<const uint16_t*>(v) + h0 * n_kv * kHeadDim, dense ? ids : ids + r0 * samples,
-                           dense ? logw : logw + r0 * samples, static_cast<uint16_t*>(out) + h0 * n * kHeadDim,
-                           lse ? lse + h0 * n : nullptr, n, n_kv, qb, hc * qb, static_cast<int>(n_kv / kKvBlock),
-                           static_cast<int>(samples), scale_log2, order);
+    const int64_t gens_per_launch = (generations + launches - 1) / launches;
+    for (int64_t g0 = 0; g0 < generations; g0 += gens_per_launch) {
+        const int64_t slot_base = g0 * 64;
+        const int64_t count = std::min(gens_per_launch * 64, slots - slot_base);
+        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(count * 8)), dim3(kPfThreads), kLdsBytes, stream,
+                           static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                           static_cast<const uint16_t*>(v), ids, logw, static_cast<uint16_t*>(out), lse, n, n_kv, qb,
+                           rows, static_cast<int>(n_kv / kKvBlock), static_cast<int>(samples), scale_log2, order,
+                           slot_base);
         if (int rc = check_launch("prefill_kernel")) return rc;
     }
     return 0;

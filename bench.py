@@ -14,10 +14,10 @@ Reported (one JSON line on stdout):
                  is the host clock over the same steps, synchronised on both
                  sides, divided by --steps;
   roofline       the prefill kernel (the dominant one): F_pre / its median
-                 duration (HIP events around its launches: the heads of a
-                 call are launched in balanced chunks of ~11,000 rows, 5 at
-                 c2, so this equals the per-launch work over the mean launch
-                 duration) vs the bf16 dense MFMA peak; traffic = HBM bytes
+                 duration (HIP events around its launches: the rows of a
+                 call are launched in chunks of ~11,000, 5 at c2, so this
+                 equals the per-launch work over the mean launch duration)
+                 vs the bf16 dense MFMA peak; traffic = HBM bytes
                  per launch from the committed rocprofv3 counter runs
                  (profiles/), or null;
   selection      build_plan's median duration, and the reference-dataflow
@@ -58,8 +58,8 @@ def work_figures(bh: int, n: int, samples: int):
     return rows, fb, f_pre, b_sel
 
 
-# Rows per prefill launch: the library launches the heads of a call in
-# balanced chunks of about this many rows (kRowsPerLaunch, csrc/prefill.hip).
+# Rows per prefill launch: the library launches the rows of a call in chunks
+# of about this many rows (kRowsPerLaunch, csrc/prefill.hip).
 ROWS_PER_PREFILL_LAUNCH = 11000
 
 
@@ -232,9 +232,9 @@ def main() -> int:
     sel = statistics.median(sel_ms)
     pre = statistics.median(pre_ms)
 
-    # Per launch: the launches are balanced (equal head counts, the last may
-    # be smaller), so F_pre / launches over the mean launch duration equals
-    # F_pre over the prefill's total duration.
+    # Per launch: the launches cover equal numbers of whole generations of
+    # rows (the last may be smaller), so F_pre / launches over the mean launch
+    # duration is F_pre over the prefill's total duration.
     launches = prefill_launches(bh, -(-n // 128))
     achieved = f_pre / (pre * 1e-3) / 1e12
     result = {

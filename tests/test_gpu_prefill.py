@@ -173,9 +173,10 @@ def test_prefill_neg_inf_blocks(oracle_mod):
 
 def test_prefill_launch_chunks(oracle_mod):
     """91 heads x 128 query blocks = 11,648 rows: the prefill runs as two
-    launches of 46 and 45 heads. Every row must be written once (the output
-    starts as NaN) and rows on both sides of the chunk boundary, the first
-    and the last, match the oracle."""
+    launches of whole generations (64 row slots per XCD, 16 slots per head on
+    each XCD), the first covering heads 0-47. Every row must be written once
+    (the output starts as NaN) and rows of heads 47 and 48, the first and the
+    last, match the oracle."""
     from ab_attention import _lib
 
     rng = np.random.default_rng(41)
@@ -195,7 +196,7 @@ def test_prefill_launch_chunks(oracle_mod):
                                        _lib.ptr(logw_d), samples, _lib.ptr(out), _lib.ptr(lse), _lib.stream(qd.device)))
     torch.cuda.synchronize()
     assert bool(torch.isfinite(out).all()) and bool(torch.isfinite(lse).all())
-    keep = np.array([0, 46 * 128 - 1, 46 * 128, 46 * 128 + 1, rows - 1])
+    keep = np.array([0, 47 * 128 + 5, 48 * 128 - 1, 48 * 128, 48 * 128 + 77, rows - 1])
     ref_o, ref_l = oracle_mod.prefill(q.float().numpy().reshape(heads, n, 128), k.float().numpy().reshape(heads, n, 128),
                                       v.float().numpy().reshape(heads, n, 128), ids, logw, rows=keep)
     got, got_l = out.float().cpu().numpy().reshape(heads, n, 128), lse.cpu().numpy().reshape(heads, n)
