@@ -130,3 +130,18 @@ def test_lse_budget_sets_head_chunks(monkeypatch):
     assert attention._heads_per_chunk(80, 591, 75600) == 1
     monkeypatch.setattr(attention, "LSE_BUDGET_BYTES", 16 * 1024 ** 3)
     assert attention._heads_per_chunk(80, 591, 75600) == 80
+
+
+def test_compact_plan_round_trip():
+    """int16 plan ids are exact for every id a head can have (0..32,767)."""
+    import torch
+    from ab_attention import SamplePlan
+    from ab_attention.video import compact_plan, expand_plan
+
+    ids = torch.arange(0, 32768, dtype=torch.int32).reshape(32, 32, 32)
+    w = torch.rand(32, 32, 32)
+    c = compact_plan(SamplePlan(ids, w))
+    assert c.descriptor.dtype == torch.int16 and c.descriptor.element_size() == 2
+    back = expand_plan(c)
+    assert back.descriptor.dtype == torch.int32 and torch.equal(back.descriptor, ids)
+    assert torch.equal(back.log_weights, w)

@@ -231,21 +231,27 @@ def test_apply_plan_in_hip_graph():
         assert torch.equal(static_lse, want_lse)
 
 
-def test_video_attention_offloaded_plans():
+@pytest.mark.parametrize("compact", [False, True])
+def test_video_attention_offloaded_plans(compact):
     """offload=True keeps each layer's plan in pinned host memory (the
-    reference's _store_plan, video.py:43-50) and copies it back on reuse; the
-    outputs equal the device-resident schedule's at every step."""
+    reference's _store_plan, video.py:43-50) and copies it back on reuse,
+    with int16 ids when compact=True; the outputs equal the device-resident
+    schedule's at every step, and so do the compact plans kept on the GPU."""
     torch.manual_seed(31)
     n, pages, layer = 2048, 2, 2
-    on_gpu, offloaded = VideoAttention(pages), VideoAttention(pages, offload=True)
+    on_gpu = VideoAttention(pages)
+    offloaded = VideoAttention(pages, offload=True, compact=compact)
+    compact_gpu = VideoAttention(pages, compact=True)
     for step in (11, 13, 15, 16):
-        print(f"offloaded schedule step {step}", flush=True)
-        on_gpu.step = offloaded.step = step
+        print(f"offloaded schedule step {step} compact={compact}", flush=True)
+        on_gpu.step = offloaded.step = compact_gpu.step = step
         q, k, v = (torch.randn(1, 2, n, 128).to(torch.bfloat16).cuda() for _ in range(3))
         a = on_gpu.attend(layer, q, k, v)
         b = offloaded.attend(layer, q, k, v)
+        c = compact_gpu.attend(layer, q, k, v)
         torch.cuda.synchronize()
-        assert torch.equal(a, b)
+        assert torch.equal(a, b) and torch.equal(a, c)
         stored = offloaded.plans[layer][1]
         assert stored.descriptor.device.type == "cpu" and stored.descriptor.is_pinned()
-        assert torch.equal(stored.descriptor, on_gpu.plans[layer][1].descriptor.cpu())
+        assert stored.descriptor.dtype == (torch.int16 if compact else torch.int32)
+        assert torch.equal(stored.descriptor.to(torch.int32), on_gpu.plans[layer][1].descriptor.cpu())
