@@ -27,6 +27,12 @@ Reported (one JSON line on stdout):
                  with its dense-equivalent work 4*d*N^2*B*H;
   cpu_baseline   the CPU oracle on all host threads (OpenMP) over one whole
                  head of the same workload, scaled by the head count.
+
+--power prints a different line instead: socket power and graphics clock
+(median over `amd-smi metric -p -c` readings, taken from a child process
+every 0.2 s) while each part of the call runs back to back for
+--power-seconds: the prefill on a fixed plan, build_plan, and dense
+attention.
 """
 from __future__ import annotations
 
@@ -35,7 +41,9 @@ import json
 import os
 import platform
 import statistics
+import subprocess
 import sys
+import threading
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -122,6 +130,57 @@ def cpu_baseline(q, k, v, cfg, head: int):
     }
 
 
+def _smi_reading():
+    """One amd-smi reading: (socket power in W, median graphics clock in MHz
+    over the XCDs), or None where the tool or a value is unavailable."""
+    try:
+        out = subprocess.run(["amd-smi", "metric", "-p", "-c", "--json"], capture_output=True, text=True,
+                             timeout=20).stdout
+        gpu = json.loads(out)["gpu_data"][0]
+        power = float(gpu["power"]["socket_power"]["value"])
+        clocks = [float(c["clk"]["value"]) for name, c in gpu["clock"].items() if name.startswith("gfx_")]
+        return power, statistics.median(clocks)
+    except (OSError, subprocess.SubprocessError, ValueError, KeyError, IndexError, TypeError,
+            statistics.StatisticsError):
+        return None
+
+
+def power_legs(legs, seconds: float):
+    """Socket power and clock while each leg runs back to back for `seconds`
+    (the first two readings of a leg are dropped as ramp-up)."""
+    import torch
+
+    out = {}
+    for name, fn in legs:
+        fn()
+        torch.cuda.synchronize()
+        readings, stop = [], threading.Event()
+
+        def sample():
+            while not stop.is_set():
+                r = _smi_reading()
+                if r is not None:
+                    readings.append(r)
+                stop.wait(0.2)
+
+        th = threading.Thread(target=sample, daemon=True)
+        th.start()
+        t0, calls = time.perf_counter(), 0
+        while time.perf_counter() - t0 < seconds:
+            fn()
+            torch.cuda.synchronize()
+            calls += 1
+        elapsed = time.perf_counter() - t0
+        stop.set()
+        th.join()
+        steady = readings[2:] or readings
+        out[name] = {"calls": calls, "ms_per_call": round(elapsed * 1e3 / calls, 3), "readings": len(steady),
+                     "socket_w": statistics.median(r[0] for r in steady) if steady else None,
+                     "gfx_mhz": statistics.median(r[1] for r in steady) if steady else None}
+        print(f"power leg {name}: {out[name]}", file=sys.stderr, flush=True)
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -137,6 +196,9 @@ def main() -> int:
                     help="IBCS head-chunk budget (default: the library's 16 GiB; the reference uses 1.5)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy (HBM counter calibration)")
+    ap.add_argument("--power", action="store_true",
+                    help="only report socket power and graphics clock per part of the call (amd-smi)")
+    ap.add_argument("--power-seconds", type=float, default=10.0)
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: every GPU box here has one GPU, and the path shards by "
@@ -191,6 +253,19 @@ def main() -> int:
                     plan.log_weights.reshape(rows, samples), order)
 
     stream = torch.cuda.current_stream()
+
+    if args.power:
+        from ab_attention.paged import _prefill
+        from ab_attention.video import exact_attention
+
+        plan = build_plan(q, k, sample_pages=cfg.sample_pages, seed=42)
+        ids, weights, order = prefill_inputs(plan)
+        legs = [("prefill", lambda: _prefill(q, k, v, ids, weights, order, False)),
+                ("selection", lambda: build_plan(q, k, sample_pages=cfg.sample_pages, seed=42))]
+        if not cfg.text_tokens:
+            legs.append(("dense", lambda: exact_attention(q, k, v)))
+        print(json.dumps({"workload": cfg.name, "power": power_legs(legs, args.power_seconds)}), flush=True)
+        return 0
 
     def step():
         plan = build_plan(q, k, sample_pages=cfg.sample_pages, seed=42)
