@@ -184,7 +184,7 @@ def power_legs(legs, seconds: float):
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=2, help="BASELINE config index (default 2)")
     ap.add_argument("--heads", type=int, default=None, help="override head count (profiling only)")
