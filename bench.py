@@ -202,7 +202,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: every GPU box here has one GPU, and the path shards by "
-              "heads with no communication (see DESIGN.md); run with --gpus 1", file=sys.stderr)
+              "heads with no communication between GPUs; run with --gpus 1", file=sys.stderr)
         return 2
 
     import torch
