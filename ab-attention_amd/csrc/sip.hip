@@ -32,7 +32,8 @@
 //     bitmask.
 // The fused plan (sip_fused_kernel, below) computes each row's masses into
 // LDS from the pair-LSEs and samples it there; rows too large for the full
-// prefix array keep two prefixes per chunk (coarse_draws).
+// prefix array keep a power-of-two number of prefixes per chunk
+// (coarse_draws).
 #include <algorithm>
 
 #include "common.hpp"
@@ -119,6 +120,25 @@ struct SipShared {
     int exact;  // coarse prefixes: the row needs the reference's probe sequence
 };
 
+constexpr size_t kSipLdsLimit = 160 * 1024;
+
+// LDS layout of the fused kernel for rows whose full prefix array does not
+// fit: the masses (16-byte aligned), then the kept prefixes.
+__host__ __device__ constexpr size_t sip_fused_coarse_offset(int64_t population) {
+    return (size_t(population + 8) * 4 + 15) / 16 * 16;
+}
+
+// Prefixes each chunk keeps, its first (the scan value) included: the largest
+// power of two (at most 32, a chunk's bucket count at the largest rows) that
+// fits the LDS left after the masses, and at least 2.
+__host__ __device__ constexpr int coarse_keep(int64_t population) {
+    const size_t used = sizeof(SipShared) + sip_fused_coarse_offset(population);
+    const size_t room = used < kSipLdsLimit ? (kSipLdsLimit - used) / (kSipThreads * sizeof(double)) : 0;
+    int keep = 2;
+    while (keep < 32 && size_t(2 * keep) <= room) keep *= 2;
+    return keep;
+}
+
 // Thread-strided partial (sum, max) over the non-certain masses: thread t
 // folds i = t, t+256, ... in order (sip.cu:63-71). The kUnroll loads of a
 // step are issued together (clamped indices), then folded. With
@@ -161,14 +181,16 @@ __device__ __forceinline__ void strided_partials(const R& rv, int pop, double& s
     mx = static_cast<double>(__uint_as_float(top));
 }
 
-// Bucket prefixes and draws from coarse prefixes (the tail of sip_row for
+// Bucket prefixes and draws from kept prefixes (the tail of sip_row for
 // kCoarse). The reference's bucket prefixes (sip.cu:131-142) are one fp64
 // chain per chunk of 4*cb blocks: prefix[b] = R (residual count) if bucket b
 // starts past the last non-certain block, else the chain E[c] + the chunk's
-// masses before bucket b, added in order. Only three prefixes per chunk are
-// kept: its first (E[c] = sh.part[c] after the scan), its middle (bucket
-// c*cb + ceil(cb/2)) and its last; any other is the same chain continued from
-// the nearest kept one, which gives the same bits.
+// masses before bucket b, added in order. Each chunk keeps `keep` of them
+// (coarse_keep: as many as the LDS holds after the masses, a power of two):
+// its first (E[c] = sh.part[c] after the scan) and those at buckets
+// c*cb + j*step, step = ceil(cb / keep); a slot whose bucket lies past the
+// chunk holds the next chunk's first prefix. Any other prefix is the same
+// chain continued from the nearest kept one, which gives the same bits.
 // A draw with threshold th (sip.cu:144-166) needs the bucket the reference's
 // binary search returns. Chains only grow, so the prefix array can fall only
 // where a chunk's last prefix exceeds the next chunk's first (rounding of the
@@ -176,7 +198,7 @@ __device__ __forceinline__ void strided_partials(const R& rv, int pop, double& s
 // If no threshold lies in such a drop at a chunk boundary, exactly one bucket
 // b has prefix[b] <= th < prefix[b + 1], and the binary search returns it
 // whatever its probes: the draw then finds it with a binary search over the
-// kept prefixes and a walk of at most ceil(cb/2) buckets. Each chunk checks
+// kept prefixes and a walk of fewer than `step` buckets. Each chunk checks
 // its boundary; a row where some threshold lands in a drop (sh.exact) makes
 // the reference's probes instead, each prefix rebuilt from the kept ones.
 template <int kWorkers, class R, class StageNext>
@@ -186,14 +208,14 @@ __device__ __forceinline__ void coarse_draws(R& rv, double* coarse, SipShared& s
                                              StageNext stage_next) {
     const int t = threadIdx.x;
     const int buckets = (pop + kBucket - 1) / kBucket;
-    const int cb = chunk / kBucket;   // buckets per chunk
-    const int half = (cb + 1) / 2;    // chunk-relative middle bucket
+    const int cb = chunk / kBucket;  // buckets per chunk
+    const int keep = coarse_keep(pop);
+    const int keep_log2 = __builtin_ctz(keep);
+    const int step = (cb + keep - 1) / keep;  // buckets between kept prefixes
     const double rd = static_cast<double>(residuals);
     const double offset = static_cast<double>(offset_u);
-    double* mid = coarse;                // [256] prefix at each chunk's middle bucket
-    double* tail = coarse + kSipThreads;  // [256] prefix at each chunk's last bucket
+    double* kept = coarse;  // [256][keep]: chunk c's prefixes at buckets c*cb + j*step
     auto chunk_end = [&](int c) { return min((c + 1) * cb, buckets); };
-    auto mid_bucket = [&](int c) { return min(c * cb + half, chunk_end(c)); };
     // prefix[c * cb]: the chunk's scan value, or R past the last residual
     // (and for the terminal bucket).
     auto first_prefix = [&](int c) -> double {
@@ -214,10 +236,15 @@ __device__ __forceinline__ void coarse_draws(R& rv, double* coarse, SipShared& s
         return cum;
     };
 
-    // Kept prefixes: the same chain walk as the reference's prefix pass.
+    // Kept prefixes: the same chain walk as the reference's prefix pass,
+    // recording the prefix at every step-th bucket of the chunk.
     if (t < kSipThreads) {
         const int begin = t * chunk, end = min(begin + chunk, pop);
-        double vmid = rd, vlast = rd;
+        double* mine = kept + t * keep;
+        mine[0] = first_prefix(t);
+        int slot = 1;          // kept prefixes of this chunk recorded so far
+        int at = step;         // chunk-relative bucket of the next one
+        double vlast = rd;     // the prefix at the chunk's last bucket
         if (begin < pop) {
             double cumulative = sh.part[t];
             int i0 = begin;
@@ -228,7 +255,10 @@ __device__ __forceinline__ void coarse_draws(R& rv, double* coarse, SipShared& s
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         if (e % kBucket == 0) {
-                            if ((i0 + e) / kBucket - t * cb == half) vmid = cumulative;
+                            if ((i0 + e) / kBucket - t * cb == at) {
+                                mine[slot++] = cumulative;
+                                at += step;
+                            }
                             vlast = cumulative;
                         }
                         cumulative = cumulative + static_cast<double>(R::x_of(r[e])) * scale;
@@ -243,7 +273,10 @@ __device__ __forceinline__ void coarse_draws(R& rv, double* coarse, SipShared& s
                     const int i = i0 + e;
                     if (e % kBucket == 0 && i < end) {
                         const double v = i > last ? rd : cumulative;
-                        if (i / kBucket - t * cb == half) vmid = v;
+                        if (i / kBucket - t * cb == at) {
+                            mine[slot++] = v;
+                            at += step;
+                        }
                         vlast = v;
                     }
                     const bool ok = i < end && !rv.certain_of(i, r[e]);
@@ -251,9 +284,6 @@ __device__ __forceinline__ void coarse_draws(R& rv, double* coarse, SipShared& s
                     cumulative = cumulative + (ok ? m : 0.0);
                 }
             }
-            // No middle bucket inside the chunk: the kept value is the next
-            // chunk's first prefix.
-            if (mid_bucket(t) == chunk_end(t)) vmid = first_prefix(t + 1);
             // A drop at the boundary with the next chunk: does some threshold
             // offset + s (0 <= s < residuals, exact in fp64) lie in it?
             const double next = first_prefix(t + 1);
@@ -265,28 +295,25 @@ __device__ __forceinline__ void coarse_draws(R& rv, double* coarse, SipShared& s
                 if (s < rd && offset + s < vlast && offset + s >= next) atomicOr(&sh.exact, 1);
             }
         }
-        mid[t] = vmid;
-        tail[t] = vlast;
+        // Slots whose bucket lies past the chunk: the next chunk's first prefix.
+        const double next_first = first_prefix(t + 1);
+        for (; slot < keep; ++slot) mine[slot] = next_first;
     }
     lds_barrier();
 
-    // Kept prefixes in bucket order: entry k is chunk k/2's first (k even) or
-    // middle (k odd) bucket.
-    auto kept_value = [&](int k) -> double { return (k & 1) ? mid[k >> 1] : first_prefix(k >> 1); };
+    // Kept prefixes in bucket order: entry k is slot k % keep of chunk k / keep.
+    auto kept_value = [&](int k) -> double { return kept[k]; };
     auto kept_bucket = [&](int k) -> int {
-        return k >= 2 * kSipThreads ? buckets : ((k & 1) ? mid_bucket(k >> 1) : min((k >> 1) * cb, buckets));
+        if (k >= kSipThreads * keep) return buckets;
+        const int c = k >> keep_log2, j = k & (keep - 1);
+        return min(c * cb + j * step, chunk_end(c));
     };
     // prefix[b] rebuilt from the nearest kept prefix at or before it.
     auto prefix_at = [&](int b) -> double {
         if (b >= buckets || kBucket * b > last) return rd;
-        const int c = b / cb, mb = mid_bucket(c);
-        int b0 = c * cb;
-        double cum = sh.part[c];
-        if (b >= mb && mb < chunk_end(c)) {
-            b0 = mb;
-            cum = mid[c];
-        }
-        for (int bb = b0; bb < b; ++bb) cum = add_bucket(bb, cum);
+        const int c = b / cb, j = (b - c * cb) / step;
+        double cum = kept[c * keep + j];
+        for (int bb = c * cb + j * step; bb < b; ++bb) cum = add_bucket(bb, cum);
         return cum;
     };
     const bool exact = sh.exact != 0;
@@ -300,13 +327,13 @@ __device__ __forceinline__ void coarse_draws(R& rv, double* coarse, SipShared& s
 #pragma unroll
         for (int d = 0; d < kDraws; ++d) threshold[d] = offset + static_cast<double>(slot0 + d * kWorkers);
         if (!exact) {
-            // Binary search over the kept prefixes (2 per chunk), the draws in
-            // lockstep, then each walks its segment to the crossing bucket.
+            // Binary search over the kept prefixes, the draws in lockstep,
+            // then each walks its segment to the crossing bucket.
             int lower[kDraws], upper[kDraws];
 #pragma unroll
             for (int d = 0; d < kDraws; ++d) {
                 lower[d] = 0;
-                upper[d] = slot0 + d * kWorkers < residuals ? 2 * kSipThreads - 1 : 0;
+                upper[d] = slot0 + d * kWorkers < residuals ? kSipThreads * keep - 1 : 0;
             }
             bool busy = true;
             while (busy) {
@@ -720,14 +747,10 @@ __global__ __launch_bounds__(kSipWorkers) void sip_lds_kernel(
 // kCoarse = false: LDS holds the fp64 bucket prefixes and the masses (c2:
 //   113 KB, one workgroup per CU).
 // kCoarse = true, for rows whose full prefix array does not fit (c3's 29,700
-//   blocks): LDS holds the masses and two kept prefixes per chunk
-//   (coarse_draws).
+//   blocks): LDS holds the masses and coarse_keep(pop) kept prefixes per
+//   chunk (coarse_draws).
 // Two 512-thread workgroups per CU with kept prefixes were tried at c2
 // (81.9 KB each): 4.89 ms against 4.14 ms for this layout.
-__host__ __device__ constexpr size_t sip_fused_coarse_offset(int64_t population) {
-    return (size_t(population + 8) * 4 + 15) / 16 * 16;
-}
-
 template <bool kCoarse>
 __global__ __launch_bounds__(kSipWorkers) void sip_fused_kernel(
     const _Float16* __restrict__ lse, const float* __restrict__ pops, const float* __restrict__ lse_max,
@@ -812,7 +835,7 @@ int launch_lds(const float* scores, const float* offsets, int64_t rows, int pop,
 }  // namespace
 
 constexpr size_t kSipStaticLds = sizeof(SipShared);
-constexpr size_t kLdsLimit = 160 * 1024;
+constexpr size_t kLdsLimit = kSipLdsLimit;
 
 size_t sip_lds_bytes(int64_t population, bool lds_values) {
     const int64_t buckets = (population + kBucket - 1) / kBucket;
@@ -823,16 +846,18 @@ size_t sip_lds_bytes(int64_t population, bool lds_values) {
 bool sip_fits(int64_t population) { return sip_lds_bytes(population, false) + kSipStaticLds <= kLdsLimit; }
 
 // The fused kernel's LDS: the bucket prefixes and the masses, or (rows too
-// large for that) the masses and two kept prefixes per chunk.
+// large for that) the masses and coarse_keep kept prefixes per chunk.
 size_t sip_fused_lds_bytes(int64_t population, bool coarse) {
-    return coarse ? sip_fused_coarse_offset(population) + size_t(2 * kSipThreads) * sizeof(double)
+    return coarse ? sip_fused_coarse_offset(population) + size_t(kSipThreads) * coarse_keep(population) *
+                                                                 sizeof(double)
                   : sip_lds_bytes(population, true);
 }
 
 bool sip_fused_fits(int64_t population) {
     return sip_fused_lds_bytes(population, true) + kSipStaticLds <= kLdsLimit;
 }
-static_assert(sip_fused_coarse_offset(kMaxKvBlocks) + 2 * kSipThreads * sizeof(double) + kSipStaticLds <= kLdsLimit,
+static_assert(sip_fused_coarse_offset(kMaxKvBlocks) + coarse_keep(kMaxKvBlocks) * kSipThreads * sizeof(double) +
+                      kSipStaticLds <= kLdsLimit,
               "every row the API accepts fits the fused kernel's LDS");
 
 namespace {
