@@ -1,6 +1,7 @@
 // SIP on gfx950: inclusion probabilities pi = min(1, tau * m_j) with
 // sum(pi) = S, certainty blocks first (ascending, weight 0), then Madow
-// systematic draws with log2(1/pi) weights. One 256-thread workgroup per row.
+// systematic draws with log2(1/pi) weights. One 1,024-thread workgroup per
+// row, 256 of whose threads play the reference's CUB block.
 //
 // Bit-exact restatement of csrc/sip.cu:33-167. Every fp64 sum keeps the
 // reference's association, which the reference gets from CUB:
