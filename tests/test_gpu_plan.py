@@ -60,7 +60,7 @@ def test_fused_plan_ordered():
 def test_fused_plan_large_rows(n):
     """27,000 and 32,768 (the most the API accepts) blocks per row: the full
     fp64 prefix array does not fit in LDS beside the masses, so the fused kernel
-    keeps two prefixes per chunk."""
+    keeps 16 and 8 prefixes per chunk."""
     print(f"fused plan large rows n={n}", flush=True)
     torch.manual_seed(8)
     q, k = (torch.randn(1, 1, n, 128).to(torch.bfloat16).cuda() for _ in range(2))
@@ -120,3 +120,33 @@ def test_build_plan_independent_of_head_chunks(monkeypatch):
     chunked = build_plan(q, k, sample_pages=4, seed=3)
     torch.cuda.synchronize()
     _assert_same(whole.descriptor, whole.log_weights, chunked.descriptor, chunked.log_weights)
+
+
+@pytest.mark.parametrize("n,samples", [(2048, 64), (108000, 2048)])
+def test_fused_plan_with_certainty(oracle_mod, n, samples):
+    """Rows with certain blocks (pi = 1: weight 0, listed first), through the
+    full prefix array (2,048 tokens) and the kept prefixes (108,000): queries
+    share a direction and three KV4 blocks per head hold keys along it, so each
+    of those blocks takes about a third of every row's mass. The certainty
+    passes, the certain ids and the draws of the remaining mass must give the
+    same bits as _C.ibcs then _C.sip (the synthetic configs have no certain
+    blocks), and the oracle's SIP on the GPU's scores."""
+    print(f"fused plan with certainty n={n} samples={samples}", flush=True)
+    torch.manual_seed(11)
+    q = (torch.randn(1, 2, n, 128) + 1.0).to(torch.bfloat16)
+    k = torch.randn(1, 2, n, 128)
+    hot = [10, 100, 300]
+    for j in hot:
+        k[:, :, 4 * j:4 * j + 4] = 3.0
+    k = k.to(torch.bfloat16)
+    ids_f, w_f, ids_s, w_s = _both(q.cuda(), k.cuda(), samples, seed=6)
+    _assert_same(ids_f, w_f, ids_s, w_s)
+    certain = (w_f == 0).sum(dim=1)
+    assert bool((certain >= len(hot)).all()), certain.min().item()
+    assert torch.equal(ids_f[:, :len(hot)].cpu(), torch.tensor(hot, dtype=torch.int32).expand(ids_f.shape[0], -1))
+    rows = ids_f.shape[0]
+    offsets = torch.rand(rows, generator=torch.Generator().manual_seed(6))
+    scores = _C.ibcs(q.cuda(), k.cuda()).cpu().numpy()
+    ids_o, w_o = oracle_mod.sip(scores, offsets.numpy(), samples)
+    assert (ids_f.cpu().numpy() == ids_o).all()
+    assert (w_f.cpu().numpy().view("uint32") == w_o.view("uint32")).all()
