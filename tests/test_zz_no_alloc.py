@@ -5,7 +5,8 @@ the same bits. Two calls in a row, the second smaller, so the second runs
 over what the first left in the shared array: 3 heads of the Wan2.1-14B
 720p length (two head chunks of the 512 MiB array), then 2 heads of 8,192
 tokens read through a token order. A head too long for the array is
-rejected before any launch."""
+rejected before any launch. The whole call, the static plan then the prefill,
+recorded into one HIP graph replays with new inputs to the eager bits."""
 import pytest
 import torch
 
@@ -69,3 +70,55 @@ def test_static_plan_rejects_oversized_head():
                                 _lib.ptr(q), _lib.stream(q.device))
     assert rc == 1
     assert b"static scratch" in lib.ab_last_error()
+
+
+def test_static_plan_in_hip_graph():
+    """The case the entry point is for: the plan (ab_ibcs_sip_static) and the
+    prefill over it recorded into one HIP graph, with every buffer allocated
+    before capture. Each replay, after new Q/K/V and uniforms are copied into
+    the captured inputs (with eager work and synchronisations between
+    replays), equals ab_ibcs_sip with a workspace plus the prefill, bit for
+    bit."""
+    lib = _lib.load()
+    heads, n, samples = 2, 8192, 256
+    q, k, offsets = _inputs(heads, n, 3)
+    v = torch.randn(1, heads, n, 128, device="cuda").to(torch.bfloat16)
+    rows = offsets.shape[0]
+    ids = torch.empty(rows, samples, dtype=torch.int32, device="cuda")
+    w = torch.empty(rows, samples, dtype=torch.float32, device="cuda")
+    out = torch.empty_like(q)
+    lse = torch.empty(1, heads, n, dtype=torch.float32, device="cuda")
+
+    def call(stream):
+        _lib.check(lib.ab_ibcs_sip_static(_lib.ptr(q), _lib.ptr(k), None, heads, n, _lib.ptr(offsets), samples,
+                                          _lib.ptr(ids), _lib.ptr(w), stream))
+        _lib.check(lib.ab_paged_prefill(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), heads, n, _lib.ptr(ids),
+                                        _lib.ptr(w), samples, _lib.ptr(out), _lib.ptr(lse), stream))
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call(_lib.stream(q.device))  # first call on the device outside capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call(_lib.stream(q.device))
+    for i in range(3):
+        print(f"static plan graph replay {i}", flush=True)
+        g = torch.Generator(device="cuda").manual_seed(40 + i)
+        for t in (q, k, v):
+            t.copy_(torch.randn(t.shape, device="cuda", generator=g).to(torch.bfloat16))
+        offsets.copy_(torch.rand(rows, device="cuda", generator=g))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = (ids.clone(), w.clone(), out.clone(), lse.clone())
+        ids_r, w_r = _with_workspace(lib, q, k, None, offsets, samples)
+        out_r, lse_r = torch.empty_like(q), torch.empty_like(lse)
+        _lib.check(lib.ab_paged_prefill(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), heads, n, _lib.ptr(ids_r),
+                                        _lib.ptr(w_r), samples, _lib.ptr(out_r), _lib.ptr(lse_r),
+                                        _lib.stream(q.device)))
+        torch.cuda.synchronize()
+        assert torch.equal(got[0], ids_r) and torch.equal(got[1].view(torch.int32), w_r.view(torch.int32))
+        assert torch.equal(got[2].view(torch.int16), out_r.view(torch.int16)) and torch.equal(got[3], lse_r)
