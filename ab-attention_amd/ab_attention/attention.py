@@ -21,10 +21,28 @@ from typing import NamedTuple
 
 import torch
 
+_BUDGET_ENV = "AB_ATTENTION_LSE_BUDGET_BYTES"
+
+
+def _budget_from_env(default: int) -> int:
+    """The pair-LSE budget from ``AB_ATTENTION_LSE_BUDGET_BYTES`` (an integer
+    or a float such as ``1.5e9``, in bytes), or ``default`` when unset."""
+    raw = os.environ.get(_BUDGET_ENV)
+    if raw is None or not raw.strip():
+        return default
+    try:
+        value = float(raw)
+    except ValueError:
+        raise ValueError(f"{_BUDGET_ENV}={raw!r} is not a byte count (an integer or a float like 1.5e9)") from None
+    if not math.isfinite(value) or value <= 0:
+        raise ValueError(f"{_BUDGET_ENV}={raw!r} must be a positive, finite byte count")
+    return int(value)
+
+
 # Budget for the [rows, 8, ~tokens/4] fp16 pair-LSEs of one head chunk; the
 # whole IBCS workspace of a chunk is about 1.07 times this (plus pooled keys
 # and centroids). At least one head is processed per chunk.
-LSE_BUDGET_BYTES = int(os.environ.get("AB_ATTENTION_LSE_BUDGET_BYTES", 16 * 1024 ** 3))
+LSE_BUDGET_BYTES = _budget_from_env(16 * 1024 ** 3)
 
 
 class SamplePlan(NamedTuple):
@@ -50,15 +68,18 @@ def _heads_per_chunk(batch_heads: int, q_blocks: int, tokens: int) -> int:
 
 @torch.no_grad()
 def build_plan(q, k, *, sample_pages=64, seed=42):
-    """Score and sample ``sample_pages * 128`` keys per 128-query block.
+    """Choose, for every block of 128 queries, the KV4 blocks it attends to.
 
-    Q and K must have shape [batch, heads, tokens, 128], bf16, on the same
-    GPU; tokens must be divisible by 4 and exceed the sampled key count.
-    IBCS scores KV4 blocks through 8 query-cluster centroids and pooled key
-    pairs; SIP draws ``sample_pages * 32`` blocks without replacement and
-    returns log2(1/pi) weights used as logit shifts at attention time.
-    Returns a ``SamplePlan`` with both tensors shaped [rows, pages, 32].
-    (Reference: attention.py:26-82.)
+    Inputs: bf16 tensors of shape [batch, heads, tokens, 128] on one GPU,
+    with a token count that is a multiple of 4 and larger than the
+    ``128 * sample_pages`` keys kept per query block. Each query block is
+    reduced to 8 centroids, each KV4 block to 2 averaged key pairs; the
+    centroids' softmax over the key pairs gives every KV4 block a mass, and
+    systematic sampling proportional to those masses keeps
+    ``32 * sample_pages`` distinct blocks per query block. Each kept block
+    carries log2 of its inverse inclusion probability, added to its logits
+    when the plan is applied. The result is a ``SamplePlan`` whose two
+    tensors are [rows, sample_pages, 32]. (Reference: attention.py:26-82.)
     """
     return _build_plan(q, k, sample_pages, seed)
 

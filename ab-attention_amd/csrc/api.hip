@@ -35,6 +35,7 @@ int launch_sip_fused(const void* lse, const float* pops, const float* lse_max, c
 int launch_prefill(const void* q, const void* k, const void* v, bool dense, int64_t bh, int64_t n, int64_t n_kv,
                    const int32_t* ids, const float* logw, int64_t samples, void* out, float* lse,
                    const int32_t* order, hipStream_t stream);
+int64_t prefill_launch_slots(int64_t bh, int64_t n);
 int launch_remap_ids(const int32_t* ids, int64_t count, const int32_t* map, int64_t map_len, int32_t* out,
                      hipStream_t stream);
 int launch_merge(const void* oa, const float* sa, const void* ob, const float* sb, int64_t count, void* out,
@@ -241,21 +242,34 @@ size_t ab_ibcs_sip_workspace_bytes(int64_t batch_heads, int64_t tokens) {
 
 }  // extern "C"
 
+namespace ab {
+// Every check of ab_ibcs_sip except the workspace's: shape, sample count,
+// pointers and alignment. Shared with the static-scratch entry point, which
+// runs it before it touches the device.
+int check_ibcs_sip_args(const char* what, const void* q, const void* k, int64_t batch_heads, int64_t tokens,
+                        const float* offsets, int64_t samples, const int32_t* ids, const float* log_weights) {
+    if (int rc = check_qk_shape(what, batch_heads, tokens)) return rc;
+    const int64_t fb = tokens / kKvBlock;
+    if (!(samples > 0 && samples < fb))
+        return set_error(AB_ERR_INVALID, "%s: sample count must be inside the population", what);
+    if (!sip_fused_fits(fb))
+        return set_error(AB_ERR_INVALID, "%s: population exceeds the fused kernel's LDS capacity", what);
+    if (!q || !k || !offsets || !ids || !log_weights) return set_error(AB_ERR_INVALID, "%s: null pointer", what);
+    if (!aligned16(q) || !aligned16(k)) return set_error(AB_ERR_INVALID, "%s: q and k must be 16-byte aligned", what);
+    return AB_OK;
+}
+}  // namespace ab
+
 namespace {
 // ab_ibcs_sip; force_exact selects the reference's probe sequence for every
 // row sampled with kept prefixes (same bits, testing only).
 int ibcs_sip_impl(const void* q, const void* k, const int32_t* order, int64_t batch_heads, int64_t tokens,
                   const float* offsets, int64_t samples, void* workspace, size_t workspace_bytes, int32_t* ids,
                   float* log_weights, int force_exact, void* stream) {
-    if (int rc = check_qk_shape("ibcs_sip", batch_heads, tokens)) return rc;
+    if (int rc = check_ibcs_sip_args("ibcs_sip", q, k, batch_heads, tokens, offsets, samples, ids, log_weights))
+        return rc;
     const IbcsLayout L = ibcs_layout(batch_heads, tokens);
-    if (!(samples > 0 && samples < L.fb))
-        return set_error(AB_ERR_INVALID, "ibcs_sip: sample count must be inside the population");
-    if (!sip_fused_fits(L.fb))
-        return set_error(AB_ERR_INVALID, "ibcs_sip: population exceeds the fused kernel's LDS capacity");
-    if (!q || !k || !offsets || !workspace || !ids || !log_weights)
-        return set_error(AB_ERR_INVALID, "ibcs_sip: null pointer");
-    if (!aligned16(q) || !aligned16(k)) return set_error(AB_ERR_INVALID, "ibcs_sip: q and k must be 16-byte aligned");
+    if (!workspace) return set_error(AB_ERR_INVALID, "ibcs_sip: null pointer");
     const size_t need = ab_ibcs_sip_workspace_bytes(batch_heads, tokens);
     if (workspace_bytes < need)
         return set_error(AB_ERR_INVALID, "ibcs_sip: workspace of %zu bytes is smaller than the %zu required",
@@ -369,6 +383,11 @@ int ab_paged_prefill_ordered(const void* q, const void* k, const void* v, const 
         return set_error(AB_ERR_INVALID, "paged_prefill: samples must be a positive multiple of 32");
     return paged_prefill_checked(q, k, v, false, order, batch_heads, tokens, tokens, ids, log_weights, samples,
                                  out, lse, stream);
+}
+
+int64_t ab_prefill_launch_slots(int64_t batch_heads, int64_t q_tokens) {
+    if (batch_heads <= 0 || q_tokens <= 0) return 0;
+    return prefill_launch_slots(batch_heads, q_tokens);
 }
 
 int ab_remap_ids(const int32_t* ids, int64_t count, const int32_t* map, int64_t map_len, int32_t* out,

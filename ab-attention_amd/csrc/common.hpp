@@ -77,4 +77,8 @@ int check_launch(const char* what);
 int ensure_lds_limit(const void* fn, int bytes);
 // Compute units of the current device (cached per device).
 int device_cu_count();
+// ab_ibcs_sip's argument checks except the workspace (shape, sample count,
+// pointers, alignment); `what` prefixes the error message.
+int check_ibcs_sip_args(const char* what, const void* q, const void* k, int64_t batch_heads, int64_t tokens,
+                        const float* offsets, int64_t samples, const int32_t* ids, const float* log_weights);
 }  // namespace ab

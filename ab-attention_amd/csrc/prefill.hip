@@ -524,6 +524,17 @@ int launch_remap_ids(const int32_t* ids, int64_t count, const int32_t* map, int6
     return check_launch("remap_ids_kernel");
 }
 
+// Row slots per XCD that one prefill launch covers (a whole number of
+// generations of 64 slots): the rows of a call are split into launches of
+// about kRowsPerLaunch rows each.
+int64_t prefill_launch_slots(int64_t bh, int64_t n) {
+    const int64_t qb = (n + kQueryBlock - 1) / kQueryBlock;
+    const int64_t rows = bh * qb;
+    const int64_t generations = ((qb + 7) / 8 * bh + 63) / 64;
+    const int64_t launches = std::max<int64_t>(1, (rows + kRowsPerLaunch - 1) / kRowsPerLaunch);
+    return (generations + launches - 1) / launches * 64;
+}
+
 int launch_prefill(const void* q, const void* k, const void* v, bool dense, int64_t bh, int64_t n, int64_t n_kv,
                    const int32_t* ids, const float* logw, int64_t samples, void* out, float* lse,
                    const int32_t* order, hipStream_t stream) {
@@ -550,12 +561,9 @@ int launch_prefill(const void* q, const void* k, const void* v, bool dense, int6
     // launch: 25.0 ms; five launches of whole heads: 23.9 ms, bit-identical),
     // and whole generations leave no half-empty generation in each launch.
     const int64_t slots = per_xcd * bh;                    // row slots per XCD
-    const int64_t generations = (slots + 63) / 64;
-    const int64_t launches = std::max<int64_t>(1, (rows + kRowsPerLaunch - 1) / kRowsPerLaunch);
-    const int64_t gens_per_launch = (generations + launches - 1) / launches;
-    for (int64_t g0 = 0; g0 < generations; g0 += gens_per_launch) {
-        const int64_t slot_base = g0 * 64;
-        const int64_t count = std::min(gens_per_launch * 64, slots - slot_base);
+    const int64_t per_launch = prefill_launch_slots(bh, n);
+    for (int64_t slot_base = 0; slot_base < slots; slot_base += per_launch) {
+        const int64_t count = std::min(per_launch, slots - slot_base);
         hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(count * 8)), dim3(kPfThreads), kLdsBytes, stream,
                            static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                            static_cast<const uint16_t*>(v), ids, logw, static_cast<uint16_t*>(out), lse, n, n_kv, qb,

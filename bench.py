@@ -66,13 +66,15 @@ def work_figures(bh: int, n: int, samples: int):
     return rows, fb, f_pre, b_sel
 
 
-# Rows per prefill launch: the library launches the rows of a call in chunks
-# of about this many rows (kRowsPerLaunch, csrc/prefill.hip).
-ROWS_PER_PREFILL_LAUNCH = 11000
+def prefill_launches(bh: int, n: int) -> int:
+    """Launches the library splits one prefill call into (its own answer,
+    ab_prefill_launch_slots: row slots per XCD per launch)."""
+    from ab_attention import _lib
 
-
-def prefill_launches(bh: int, qb: int) -> int:
-    return max(1, -(-bh * qb // ROWS_PER_PREFILL_LAUNCH))
+    per_launch = _lib.load().ab_prefill_launch_slots(bh, n)
+    qb = -(-n // 128)
+    slots = -(-qb // 8) * bh  # row slots per XCD
+    return max(1, -(-slots // per_launch))
 
 
 def _traffic_from_profiles(workload: str):
@@ -310,7 +312,7 @@ def main() -> int:
     # Per launch: the launches cover equal numbers of whole generations of
     # rows (the last may be smaller), so F_pre / launches over the mean launch
     # duration is F_pre over the prefill's total duration.
-    launches = prefill_launches(bh, -(-n // 128))
+    launches = prefill_launches(bh, n)
     achieved = f_pre / (pre * 1e-3) / 1e12
     result = {
         "metric": METRIC,

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define AB_ABI_VERSION 3
+#define AB_ABI_VERSION 4
 
 enum ab_status {
     AB_OK = 0,
@@ -89,22 +89,6 @@ int ab_ibcs_sip(const void *q, const void *k, const int32_t *order, int64_t batc
                 const float *offsets, int64_t samples, void *workspace, size_t workspace_bytes, int32_t *ids,
                 float *log_weights, void *stream);
 
-/* ---- Fused plan without allocation ----------------------------------------
- * No counterpart in the reference; for callers that cannot allocate device
- * memory (code under HIP graph capture, tight serving loops, harnesses that
- * forbid hipMalloc). ab_ibcs_sip with the same arguments minus the workspace,
- * giving the same bits. The IBCS intermediates live in a static device array
- * of AB_STATIC_SCRATCH_BYTES that each GPU the library runs on holds until
- * the process ends; heads run in chunks that fit it, and a shape whose single
- * head needs more (tokens above 128,768) is rejected with AB_ERR_INVALID
- * before any launch. The call allocates nothing (no hipMalloc, no hipFree).
- * Calls that overlap on one GPU (other streams or threads) race on the
- * array. The first call on a device resolves the array's address, a runtime
- * call: make it outside graph capture. */
-#define AB_STATIC_SCRATCH_BYTES ((size_t)512 << 20)
-int ab_ibcs_sip_static(const void *q, const void *k, const int32_t *order, int64_t batch_heads, int64_t tokens,
-                       const float *offsets, int64_t samples, int32_t *ids, float *log_weights, void *stream);
-
 /* Testing variant of ab_ibcs_sip; no counterpart in the reference. Every
  * row that is sampled with kept prefixes takes the reference's binary-search
  * probes (each prefix rebuilt from the kept ones), the path otherwise taken
@@ -146,6 +130,17 @@ int ab_paged_prefill_kv(const void *q, const void *k, const void *v, int64_t bat
  * video (README.md:132-133). */
 int ab_dense_prefill(const void *q, const void *k, const void *v, int64_t batch_heads, int64_t q_tokens,
                      int64_t kv_tokens, void *out, float *lse, void *stream);
+
+/* How the prefill entry points split a call's rows into launches; no
+ * counterpart in the reference (FlashInfer runs one kernel). The rows of
+ * head h, query block b are dealt to 8 groups (one per XCD) of
+ * ceil(q_blocks / 8) consecutive blocks: group b / ceil(q_blocks / 8), row
+ * slot h * ceil(q_blocks / 8) + b % ceil(q_blocks / 8) within the group.
+ * Launch i covers the row slots [i * S, (i + 1) * S) of every group, where
+ * S = ab_prefill_launch_slots(batch_heads, q_tokens) (a multiple of 64;
+ * 0 for a non-positive size). Callers need this only to account for
+ * per-launch timings. */
+int64_t ab_prefill_launch_slots(int64_t batch_heads, int64_t q_tokens);
 
 /* ---- Attention-state merge -------------------------------------------------
  * Replaces FlashInfer's merge_state as used by _merge

@@ -595,6 +595,16 @@ int orc_prefill_kv(const float *q, const float *k, const float *v, int64_t bh_co
                     if (z > mx) mx = z;
                 }
             }
+            float *oi = out + (bh * n + i) * HEAD_DIM;
+            if (mx == -INFINITY) {
+                /* No listed key has a finite logit (every weight is -inf): the
+                 * softmax is empty, so o = 0 and lse = -inf rather than the 0/0
+                 * of the formula below. This convention is unpinned against the
+                 * reference (no fixture covers it). */
+                for (int d = 0; d < HEAD_DIM; ++d) oi[d] = 0.0f;
+                if (lse) lse[bh * n + i] = -INFINITY;
+                continue;
+            }
             double acc[HEAD_DIM] = {0}, den = 0.0;
             for (int64_t s = 0; s < samples; ++s) {
                 const int64_t j = rid[s];
@@ -605,7 +615,6 @@ int orc_prefill_kv(const float *q, const float *k, const float *v, int64_t bh_co
                     for (int d = 0; d < HEAD_DIM; ++d) acc[d] += p * (double)vt[d];
                 }
             }
-            float *oi = out + (bh * n + i) * HEAD_DIM;
             for (int d = 0; d < HEAD_DIM; ++d) oi[d] = (float)(acc[d] / den);
             if (lse) lse[bh * n + i] = (float)((mx + log(den)) / ln2);
         }

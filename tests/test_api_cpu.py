@@ -145,3 +145,19 @@ def test_compact_plan_round_trip():
     back = expand_plan(c)
     assert back.descriptor.dtype == torch.int32 and torch.equal(back.descriptor, ids)
     assert torch.equal(back.log_weights, w)
+
+
+def test_lse_budget_env_parsing(monkeypatch):
+    """AB_ATTENTION_LSE_BUDGET_BYTES takes an integer or a float byte count;
+    anything else raises a ValueError that names the variable."""
+    from ab_attention import attention
+
+    monkeypatch.delenv("AB_ATTENTION_LSE_BUDGET_BYTES", raising=False)
+    assert attention._budget_from_env(123) == 123
+    for raw, want in (("1610612736", 1610612736), ("1.5e9", 1500000000), (" 2048 ", 2048)):
+        monkeypatch.setenv("AB_ATTENTION_LSE_BUDGET_BYTES", raw)
+        assert attention._budget_from_env(123) == want
+    for raw in ("1.5GiB", "-1", "0", "nan", "inf"):
+        monkeypatch.setenv("AB_ATTENTION_LSE_BUDGET_BYTES", raw)
+        with pytest.raises(ValueError, match="AB_ATTENTION_LSE_BUDGET_BYTES"):
+            attention._budget_from_env(123)

@@ -25,7 +25,10 @@ test_c2_full_call -- the whole call through build_plan and apply_plan:
     array);
   - 64 random rows across all 80 heads are bit-exact with the oracle's SIP on
     the GPU's scores and build_plan's uniforms;
-  - the output is finite, and 8 rows across 4 heads match the oracle prefill.
+  - the output is finite; rows of every one of the prefill's 5 launches
+    (each launch's first and last row slots and the slots on both sides of
+    a generation boundary, on the first and last XCD) and 8 rows across 4
+    heads match the oracle prefill.
 """
 import numpy as np
 import pytest
@@ -59,6 +62,54 @@ def _check_rows(got, got_lse, ref, ref_lse, rows, n):
         if got_lse is not None:
             lerr = np.abs(got_lse[lo:hi] - ref_lse[lo:hi]).max()
             assert lerr <= LSE_ABS, (r, lerr)
+
+
+def launch_check_rows(bh, n):
+    """Rows to compare with the oracle in every prefill launch of a call of
+    bh heads x n tokens, as {launch: [rows]}: the first and last row slot of
+    the launch and the two slots on each side of a generation boundary in
+    its middle, each on XCD 0 and on the last XCD whose query blocks reach
+    that slot. The library deals the rows of head h, query block b to XCD
+    group b // ceil(qb / 8) at slot h * ceil(qb / 8) + b % ceil(qb / 8); launch
+    i covers the slots [i * S, (i + 1) * S) of every group, S =
+    ab_prefill_launch_slots (whole generations of 64 slots)."""
+    from ab_attention import _lib
+
+    qb = -(-n // 128)
+    per_xcd = -(-qb // 8)
+    slots = per_xcd * bh
+    per_launch = _lib.load().ab_prefill_launch_slots(bh, n)
+    picks = {}
+    for launch, s0 in enumerate(range(0, slots, per_launch)):
+        s1 = min(s0 + per_launch, slots)
+        mid = s0 + 64 * (-(-(s1 - s0) // 64) // 2)
+        rows = set()
+        for slot in sorted({s0, mid - 1, mid, s1 - 1}):
+            if not s0 <= slot < s1:
+                continue
+            head, off = divmod(slot, per_xcd)
+            rows.add(head * qb + off)  # XCD 0
+            for xcd in range(7, 0, -1):
+                if xcd * per_xcd + off < qb:
+                    rows.add(head * qb + xcd * per_xcd + off)
+                    break
+        picks[launch] = sorted(rows)
+    return picks
+
+
+def check_rows_by_head(oracle_mod, head_tensors, out_head, ids, w, rows, qb, n, tag):
+    """Compare the output rows `rows` (global plan rows) with the oracle
+    prefill, one head at a time. head_tensors(bh) -> (q, k, v) f32 [1, n, 128]
+    and out_head(bh) -> output f32 [n, 128] of that head, in the order the plan
+    indexes its tokens."""
+    rows = np.asarray(sorted(set(int(r) for r in rows)))
+    for bh_i in np.unique(rows // qb):
+        local = rows[rows // qb == bh_i] - bh_i * qb
+        head = slice(bh_i * qb, (bh_i + 1) * qb)
+        print(f"{tag}: head {bh_i} rows {local.tolist()}", flush=True)
+        qh, kh, vh = head_tensors(int(bh_i))
+        ref, _ = oracle_mod.prefill(qh, kh, vh, ids[head].cpu().numpy(), w[head].cpu().numpy(), rows=local)
+        _check_rows(out_head(int(bh_i)), None, ref[0], None, local, n)
 
 
 def _assert_sip_equal(ids_g, w_g, ids_o, w_o):
@@ -157,12 +208,14 @@ def test_c2_full_call(oracle_mod):
     assert len(np.unique(pick // qb)) > 40  # the random rows span the heads
     del scores
 
-    # the output on 8 rows across 4 heads (batch item, head) against the oracle
-    for bh_i in (0, 23, 41, 79):
-        rows_local = np.array([bh_i % qb, qb - 1]) if bh_i % 2 else np.array([qb // 2, 7])
-        bi, hi = divmod(bh_i, h)
-        qh, kh, vh = (_f32(t[bi, hi]).reshape(1, n, 128) for t in (q, k, v))
-        head_rows = slice(bh_i * qb, (bh_i + 1) * qb)
-        ids_h, w_h = ids[head_rows].cpu().numpy(), w[head_rows].cpu().numpy()
-        ref, _ = oracle_mod.prefill(qh, kh, vh, ids_h, w_h, rows=rows_local)
-        _check_rows(_f32(out[bi, hi]).reshape(n, 128), None, ref[0], None, rows_local, n)
+    # the output against the oracle: rows in every prefill launch (its first
+    # and last row slots and both sides of a generation boundary), plus rows
+    # of four heads, the ragged last query block among them
+    per_launch = launch_check_rows(bh, n)
+    assert len(per_launch) == 5 and all(len(r) >= 2 for r in per_launch.values()), per_launch
+    extra = [bh_i * qb + r for bh_i in (0, 23, 41, 79)
+             for r in ((bh_i % qb, qb - 1) if bh_i % 2 else (qb // 2, 7))]
+    check_rows_by_head(
+        oracle_mod, lambda i: tuple(_f32(t[i // h, i % h]).reshape(1, n, 128) for t in (q, k, v)),
+        lambda i: _f32(out[i // h, i % h]).reshape(n, 128), ids, w,
+        [r for rs in per_launch.values() for r in rs] + extra, qb, n, "c2 full call")

@@ -24,7 +24,7 @@ import torch
 from ab_attention import _C, apply_plan, build_plan
 from ab_attention.synthetic import CONFIGS, make_qkv
 from ab_attention.video import VideoAttention, apply_cube_plan, cube_order, cube_plan, hunyuan_attention
-from test_gpu_c2 import _assert_sip_equal, _check_rows, _f32, _sip_invariants
+from test_gpu_c2 import _assert_sip_equal, _check_rows, _f32, _sip_invariants, check_rows_by_head, launch_check_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -124,11 +124,13 @@ def test_c4_full_call_in_place(oracle_mod):
     pick = _plan_rows(oracle_mod, qc, kc, ids, w, fb, seed, "c4 full call")
     assert len(np.unique(pick // qb)) > 40
     del qc, kc
-    # the oracle sees the cube-ordered tensors; the output is read back in cube order
-    for bh_i in (5, 66):
-        bi, hi = divmod(bh_i, h)
-        keep = np.array([0, qb // 2, qb - 1])
-        head = slice(bh_i * qb, (bh_i + 1) * qb)
-        cube = [_f32(t[bi, hi].index_select(0, order)).reshape(1, n, 128) for t in (q, k, v)]
-        ref, _ = oracle_mod.prefill(*cube, ids[head].cpu().numpy(), w[head].cpu().numpy(), rows=keep)
-        _check_rows(_f32(out[bi, hi].index_select(0, order)).reshape(n, 128), None, ref[0], None, keep, n)
+    # the oracle sees the cube-ordered tensors; the output is read back in
+    # cube order. Rows of every prefill launch, and of heads 5 and 66.
+    per_launch = launch_check_rows(b * h, n)
+    assert len(per_launch) == 5 and all(len(r) >= 2 for r in per_launch.values()), per_launch
+    extra = [bh_i * qb + r for bh_i in (5, 66) for r in (0, qb // 2, qb - 1)]
+    check_rows_by_head(
+        oracle_mod,
+        lambda i: tuple(_f32(t[i // h, i % h].index_select(0, order)).reshape(1, n, 128) for t in (q, k, v)),
+        lambda i: _f32(out[i // h, i % h].index_select(0, order)).reshape(n, 128), ids, w,
+        [r for rs in per_launch.values() for r in rs] + extra, qb, n, "c4 full call")

@@ -9,22 +9,42 @@ import pytest
 
 from ab_attention import _lib
 
-HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "ab_attention.h")
+INCLUDE = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include")
 
 
-def _declared():
-    text = open(HEADER).read()
+def _declared(header):
+    text = open(os.path.join(INCLUDE, header)).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(ab_\w+)\s*\(", text)))
 
 
 def test_every_declared_symbol_is_exported():
     lib = _lib.load()
-    names = _declared()
+    names = _declared("ab_attention.h")
     assert len(names) >= 9
     for name in names:
         assert hasattr(lib, name), name
     assert sorted(_lib.SIGNATURES) == names
+
+
+def test_static_library_exports_its_header():
+    static = _lib.load_static()
+    names = _declared("ab_attention_static.h")
+    assert names == ["ab_ibcs_sip_static"] == sorted(_lib.STATIC_SIGNATURES)
+    for name in names:
+        assert hasattr(static, name), name
+    assert not hasattr(_lib.load(), "ab_ibcs_sip_static")  # the main library carries no static scratch
+
+
+def test_prefill_launch_geometry():
+    lib = _lib.load()
+    # row slots per XCD and launch: whole generations of 64
+    for bh, n, launches in ((80, 75600, 5), (24, 32760, 1), (24, 119056, 3), (2, 2048, 1), (1, 128, 1)):
+        per = lib.ab_prefill_launch_slots(bh, n)
+        slots = -(-(-(-n // 128)) // 8) * bh
+        assert per > 0 and per % 64 == 0
+        assert -(-slots // per) == launches, (bh, n, per)
+    assert lib.ab_prefill_launch_slots(0, 100) == 0
 
 
 def test_abi_version():
@@ -58,3 +78,24 @@ def test_validation_before_launch(call, msg):
     lib = _lib.load()
     assert call(lib) == 1
     assert msg in lib.ab_last_error()
+
+
+_A = 4096  # a 16-byte aligned stand-in address: every case is rejected before any runtime call
+
+
+@pytest.mark.parametrize("args,msg", [
+    ((_A, _A, None, 1, 1022, _A, 64, _A, _A, None), b"divisible by 4"),
+    ((_A, _A, None, 1, 4 * 40000, _A, 64, _A, _A, None), b"32768"),
+    ((_A, _A, None, 70000, 1024, _A, 64, _A, _A, None), b"grid too large"),
+    ((_A, _A, None, 1, 1024, _A, 300, _A, _A, None), b"inside the population"),
+    ((_A, _A, None, 1, 1024, _A, 0, _A, _A, None), b"inside the population"),
+    ((_A, None, None, 1, 1024, _A, 64, _A, _A, None), b"null pointer"),
+    ((_A, _A, None, 1, 1024, _A, 64, None, _A, None), b"null pointer"),
+    ((_A + 8, _A, None, 1, 1024, _A, 64, _A, _A, None), b"16-byte aligned"),
+    ((_A, _A, None, 1, 131072, _A, 2048, _A, _A, None), b"static scratch"),
+])
+def test_static_validation_before_launch(args, msg):
+    static = _lib.load_static()
+    assert static.ab_ibcs_sip_static(*args) == 1
+    err = _lib.load().ab_last_error()
+    assert msg in err and err.startswith(b"ibcs_sip_static:"), err

@@ -140,3 +140,31 @@ def test_merge_of_disjoint_partitions_is_attention_over_union(oracle_mod):
     o2, l2 = oracle_mod.merge_states(oa, la, ob, np.full_like(lb, -np.inf))
     np.testing.assert_allclose(o2, oa, rtol=1e-12, atol=0)
     np.testing.assert_allclose(l2, la, rtol=1e-12, atol=0)
+
+
+def test_neg_inf_weights_remove_blocks(oracle_mod):
+    """A block at weight -inf contributes nothing: the row equals attention
+    over its other blocks (those blocks dropped from the list). A row whose
+    every block is at -inf has an empty softmax: o = 0 and lse = -inf, with
+    no NaN (the convention the GPU kernel follows; no reference fixture pins
+    it)."""
+    rng = np.random.default_rng(5)
+    n, S = 512, 16
+    q, k, v = _inputs(rng, 1, n)
+    rows, fb = n // 128, n // 4
+    ids = rng.integers(0, fb, (rows, S)).astype(np.int32)
+    logw = (rng.random((rows, S)) * 2).astype(np.float32)
+    logw[0, :5] = -np.inf
+    logw[1, 3::4] = -np.inf
+    logw[2, :] = -np.inf
+    o, l = oracle_mod.prefill(q, k, v, ids, logw)
+    for r in (0, 1):
+        keep = np.isfinite(logw[r])
+        sub_ids = np.tile(ids[r][keep], (rows, 1))
+        sub_w = np.tile(logw[r][keep], (rows, 1))
+        ro, rl = _reference(q, k, v, sub_ids, sub_w)
+        sl = slice(r * 128, r * 128 + 128)
+        np.testing.assert_allclose(o[0, sl], ro[0, sl], rtol=1e-5, atol=1e-6)
+        np.testing.assert_allclose(l[0, sl], rl[0, sl], rtol=1e-6, atol=1e-5)
+    assert np.all(o[0, 256:384] == 0.0) and np.all(np.isneginf(l[0, 256:384]))
+    assert np.all(np.isfinite(o[0, 384:]))
