@@ -54,6 +54,33 @@ __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_lo
 
 __device__ __forceinline__ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// (float)half - ref for the low (kHigh = false) or high half of a packed
+// fp16 pair, in one v_fma_mix_f32: half * 1.0 + (-ref), rounded once. The
+// conversion is exact, so this equals (float)half - ref rounded, in one
+// instruction instead of a conversion and a subtraction.
+template <bool kHigh>
+__device__ __forceinline__ float f16_minus(uint32_t packed, float ref) {
+    float r;
+    if (kHigh)
+        asm("v_fma_mix_f32 %0, %1, 1.0, -%2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(packed), "v"(ref));
+    else
+        asm("v_fma_mix_f32 %0, %1, 1.0, -%2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(packed), "v"(ref));
+    return r;
+}
+// The same with a wave-uniform ref held in an SGPR (no copy to a VGPR).
+template <bool kHigh>
+__device__ __forceinline__ float f16_minus_uniform(uint32_t packed, float ref) {
+    float r;
+    if (kHigh)
+        asm("v_fma_mix_f32 %0, %1, 1.0, -%2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(packed), "s"(ref));
+    else
+        asm("v_fma_mix_f32 %0, %1, 1.0, -%2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(packed), "s"(ref));
+    return r;
+}
+#pragma clang diagnostic pop
+
 // Workgroup barrier for LDS traffic only: waits for this wave's LDS accesses
 // (lgkmcnt(0)) but leaves its outstanding global loads in flight. HIP's
 // __syncthreads() also waits for every outstanding global load (vmcnt(0)),

@@ -272,7 +272,8 @@ __global__ __launch_bounds__(kClusterThreads) void cluster_pool_kernel(
 
 // ---------------------------------------------------------------------------
 // Stage 4: population-weighted masses, one workgroup per row:
-//   m_j = sum_s fmaf(n_s, exp2(l_sj - M_s) * (1/D_s), .) * (1 / sum_s n_s).
+//   m_j = sum_s fmaf(n_s / D_s, exp2(l_sj - M_s), .) * (1 / sum_s n_s)
+// (RowMasses in masses.hpp).
 
 constexpr int kMassThreads = 256;
 

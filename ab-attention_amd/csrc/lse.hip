@@ -75,18 +75,6 @@ __device__ __forceinline__ void lds_dma16_after_reads(const void* base, uint32_t
 }
 #pragma clang diagnostic pop
 
-// (float)half - ref for the low (kHigh = false) or high half of a packed
-// fp16 pair, in one v_fma_mix_f32: half * 1.0 + (-ref), rounded once.
-template <bool kHigh>
-__device__ __forceinline__ float f16_minus(uint32_t packed, float ref) {
-    float r;
-    if (kHigh)
-        asm("v_fma_mix_f32 %0, %1, 1.0, -%2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(packed), "v"(ref));
-    else
-        asm("v_fma_mix_f32 %0, %1, 1.0, -%2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(packed), "v"(ref));
-    return r;
-}
-
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt range");

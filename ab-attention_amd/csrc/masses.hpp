@@ -1,12 +1,17 @@
 // Population-weighted KV4 block masses of one row (reference:
 // csrc/ibcs.cu:495-538):
-//   m_j = sum_s fmaf(n_s, exp2(l_sj - M_s) * (1/D_s), .) * (1 / sum_s n_s)
+//   m_j = sum_s fmaf(c_s, exp2(l_sj - M_s), .) * (1 / sum_s n_s),
+//   c_s = n_s * (1/D_s) (rounded once per row and centroid)
 // from the fp16 pair-LSEs l [8, ld] of the row, the populations n_s and the
-// per-centroid maxima M_s and normalisers D_s. Shared by the masses kernel
-// (scores to global memory) and the fused masses + SIP kernel (scores into
-// LDS), so both produce the same bits: the same operations in the same order,
-// every product rounded before its sum (the library builds with
-// -ffp-contract=off).
+// per-centroid maxima M_s and normalisers D_s. The reference forms
+// n_s * (exp2(l - M_s) / D_s) per element; folding n_s / D_s into one
+// coefficient per row changes a mass by about one float ulp (within the
+// tolerance against the CPU oracle) and saves a multiplication per element,
+// and l - M_s is one v_fma_mix_f32 (exact conversion, one rounding): three
+// instructions per (centroid, block) instead of five. Shared by the masses
+// kernel (scores to global memory) and the fused masses + SIP kernel (scores
+// into LDS), so both produce the same bits: the same operations in the same
+// order (the library builds with -ffp-contract=off).
 #pragma once
 
 #include "common.hpp"
@@ -15,8 +20,10 @@ namespace ab {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
+// The constants of one row; every thread of a workgroup holds the same row,
+// so they are wave-uniform (SGPRs).
 struct RowMasses {
-    float weight[kCentroids], inv_den[kCentroids], mx[kCentroids];
+    float coef[kCentroids], mx[kCentroids];
     float inv_total;
 
     __device__ __forceinline__ void load(const float* __restrict__ pops, const float* __restrict__ lse_max,
@@ -24,10 +31,10 @@ struct RowMasses {
         float total = 0.0f;
 #pragma unroll
         for (int s = 0; s < kCentroids; ++s) {
-            weight[s] = pops[row * kCentroids + s];
-            inv_den[s] = __fdiv_rn(1.0f, lse_den[row * kCentroids + s]);
+            const float weight = pops[row * kCentroids + s];
+            coef[s] = weight * __fdiv_rn(1.0f, lse_den[row * kCentroids + s]);
             mx[s] = lse_max[row * kCentroids + s];
-            total += weight[s];
+            total += weight;
         }
         inv_total = __fdiv_rn(1.0f, total);
     }
@@ -38,11 +45,17 @@ struct RowMasses {
 #pragma unroll
         for (int e = 0; e < 8; ++e) score[e] = 0.0f;
 #pragma unroll
-        for (int s = 0; s < kCentroids; ++s)
+        for (int s = 0; s < kCentroids; ++s) {
+            // The whole vector is bit-cast (never one element of it).
+            const u32x4 pairs = __builtin_bit_cast(u32x4, h[s]);
 #pragma unroll
-            for (int e = 0; e < 8; ++e)
-                score[e] =
-                    __builtin_fmaf(weight[s], fast_exp2(static_cast<float>(h[s][e]) - mx[s]) * inv_den[s], score[e]);
+            for (int e = 0; e < 4; ++e) {
+                score[2 * e] =
+                    __builtin_fmaf(coef[s], fast_exp2(f16_minus_uniform<false>(pairs[e], mx[s])), score[2 * e]);
+                score[2 * e + 1] =
+                    __builtin_fmaf(coef[s], fast_exp2(f16_minus_uniform<true>(pairs[e], mx[s])), score[2 * e + 1]);
+            }
+        }
 #pragma unroll
         for (int e = 0; e < 8; ++e) out[e] = score[e] * inv_total;
     }

@@ -74,6 +74,11 @@ struct LdsRow {
     __device__ __forceinline__ static float x_of(float r) {
         return __uint_as_float(max(__float_as_uint(r) & 0x7fffffffu, __float_as_uint(1e-30f)));
     }
+    // x_of for a row with no element marked: every stored value has its sign
+    // bit clear, so the mask is not needed.
+    __device__ __forceinline__ static float x_unmarked(float r) {
+        return __uint_as_float(max(__float_as_uint(r), __float_as_uint(1e-30f)));
+    }
     __device__ __forceinline__ bool certain_of(int, float r) const { return (__float_as_uint(r) >> 31) != 0u; }
     __device__ __forceinline__ float x(int i) const { return x_of(values[i]); }
     __device__ __forceinline__ bool certain(int i) const { return certain_of(i, values[i]); }
@@ -96,6 +101,7 @@ struct GlobalRow {
         for (int e = 0; e < 8; ++e) r[e] = input[min(i0 + e, last)];
     }
     __device__ __forceinline__ static float x_of(float r) { return fmaxf(r, 1e-30f); }
+    __device__ __forceinline__ static float x_unmarked(float r) { return x_of(r); }
     __device__ __forceinline__ bool certain_of(int i, float) const {
         return any_certain && ((marks[i >> 5] >> (i & 31)) & 1u);
     }
@@ -160,7 +166,7 @@ __device__ __forceinline__ void strided_partials(const R& rv, int pop, double& s
             for (int e = 0; e < kUnroll; ++e) r[e] = rv.raw(i0 + e * kSipThreads);
 #pragma unroll
             for (int e = 0; e < kUnroll; ++e) {
-                const float x = R::x_of(r[e]);
+                const float x = R::x_unmarked(r[e]);
                 sum = sum + static_cast<double>(x);
                 top = max(top, __float_as_uint(x));
             }
@@ -262,7 +268,7 @@ __device__ __forceinline__ void coarse_draws(R& rv, double* coarse, SipShared& s
                             }
                             vlast = cumulative;
                         }
-                        cumulative = cumulative + static_cast<double>(R::x_of(r[e])) * scale;
+                        cumulative = cumulative + static_cast<double>(R::x_unmarked(r[e])) * scale;
                     }
                 }
             }
@@ -534,7 +540,7 @@ __device__ __forceinline__ void sip_row(R& rv, double sum, double mx, double* pr
                 rv.raw8(i0, r);
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
-                    chunk_mass = chunk_mass + static_cast<double>(R::x_of(r[e])) * scale;
+                    chunk_mass = chunk_mass + static_cast<double>(R::x_unmarked(r[e])) * scale;
             }
         }
         for (; i0 < end; i0 += 8) {
@@ -594,7 +600,7 @@ __device__ __forceinline__ void sip_row(R& rv, double sum, double mx, double* pr
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     if (e % kBucket == 0) prefix[(i0 + e) / kBucket] = cumulative;
-                    cumulative = cumulative + static_cast<double>(R::x_of(r[e])) * scale;
+                    cumulative = cumulative + static_cast<double>(R::x_unmarked(r[e])) * scale;
                 }
             }
         }
@@ -783,11 +789,19 @@ __global__ __launch_bounds__(kSipWorkers) void sip_fused_kernel(
             for (int u = 0; u < 2; ++u) {
                 const int g = g0 + u * kSipWorkers;
                 if (g < groups) {
+                    // Whole groups of 8: the masses of a last partial group
+                    // past the population land in values[]' 8 padding
+                    // entries, which no reader uses.
                     float m[8];
                     rm.eight(h[u], m);
+                    f32x4 lo, hi;
 #pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        if (8 * g + e < pop) values[8 * g + e] = m[e] > 0.0f ? m[e] : 0.0f;  // NaN, negatives -> +0
+                    for (int e = 0; e < 4; ++e) {
+                        lo[e] = m[e] > 0.0f ? m[e] : 0.0f;  // NaN, negatives -> +0
+                        hi[e] = m[e + 4] > 0.0f ? m[e + 4] : 0.0f;
+                    }
+                    *reinterpret_cast<f32x4*>(values + 8 * g) = lo;
+                    *reinterpret_cast<f32x4*>(values + 8 * g + 4) = hi;
                 }
             }
         }
