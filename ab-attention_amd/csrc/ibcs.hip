@@ -82,9 +82,16 @@ __device__ __forceinline__ int block_argmax(float value, int index, float* s_val
     return (v1 > v0 || (v1 == v0 && i1 < i0)) ? i1 : i0;
 }
 
-__device__ __forceinline__ float block_elem(const uint32_t* block, int row, int dim) {
-    const uint32_t w = block[row * kRowWords + (dim >> 1)];
-    return (dim & 1) ? bf16_hi(w) : bf16_lo(w);
+// Byte selector of v_perm_b32 that moves the bf16 of dim `dim` of a packed
+// pair into the high half of a float (low half zero): bytes 1,0 for an even
+// dim, 3,2 for an odd one (0x0c selects a zero byte).
+__device__ __forceinline__ uint32_t bf16_select(int dim) { return (dim & 1) ? 0x03020c0cu : 0x01000c0cu; }
+
+// block_elem for a per-lane dim, with the selector precomputed: one v_perm_b32
+// instead of both conversions and a select.
+__device__ __forceinline__ float block_elem_sel(const uint32_t* block, int row, int word, uint32_t sel) {
+    const uint32_t w = block[row * kRowWords + word];
+    return __uint_as_float(__builtin_amdgcn_perm(w, w, sel));
 }
 
 __global__ __launch_bounds__(kClusterThreads) void cluster_pool_kernel(
@@ -117,35 +124,38 @@ __global__ __launch_bounds__(kClusterThreads) void cluster_pool_kernel(
     // key rows 2p + (i & 1), p = r0 + 8(i/2); rows past the sequence end are
     // clamped (their loads are discarded), and every order entry is loaded
     // before any data load.
-    int64_t srow[16];
+    // Offsets in 16-byte units from the head's base (32-bit: a head has at
+    // most 131,072 tokens, 2,097,152 units).
+    const int nm1 = static_cast<int>(n - 1), b32 = static_cast<int>(base);
+    uint32_t soff[16];
     if (order) {
         int32_t o[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) o[i] = order[base + min(r0 + 8 * i, valid - 1)];
+        for (int i = 0; i < 16; ++i) o[i] = order[b32 + min(r0 + 8 * i, valid - 1)];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) srow[i] = min<int64_t>(max(o[i], 0), n - 1);
+        for (int i = 0; i < 16; ++i) soff[i] = uint32_t(min(max(o[i], 0), nm1)) * 16u + c16;
     } else {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) srow[i] = base + min(r0 + 8 * i, valid - 1);
+        for (int i = 0; i < 16; ++i) soff[i] = uint32_t(b32 + min(r0 + 8 * i, valid - 1)) * 16u + c16;
     }
-    int64_t krow[16];
+    uint32_t koff[16];
     if (order) {
         int32_t o[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) o[i] = order[base + min(2 * (r0 + 8 * (i >> 1)) + (i & 1), valid - 1)];
+        for (int i = 0; i < 16; ++i) o[i] = order[b32 + min(2 * (r0 + 8 * (i >> 1)) + (i & 1), valid - 1)];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) krow[i] = min<int64_t>(max(o[i], 0), n - 1);
+        for (int i = 0; i < 16; ++i) koff[i] = uint32_t(min(max(o[i], 0), nm1)) * 16u + c16;
     } else {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) krow[i] = base + min(2 * (r0 + 8 * (i >> 1)) + (i & 1), valid - 1);
+        for (int i = 0; i < 16; ++i) koff[i] = uint32_t(b32 + min(2 * (r0 + 8 * (i >> 1)) + (i & 1), valid - 1)) * 16u + c16;
     }
     u32x4 qv[16], ka[8], kb[8];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) qv[i] = qhead[srow[i] * 16 + c16];
+    for (int i = 0; i < 16; ++i) qv[i] = qhead[soff[i]];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        ka[i] = khead[krow[2 * i] * 16 + c16];
-        kb[i] = khead[krow[2 * i + 1] * 16 + c16];
+        ka[i] = khead[koff[2 * i]];
+        kb[i] = khead[koff[2 * i + 1]];
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i)
@@ -176,6 +186,10 @@ __global__ __launch_bounds__(kClusterThreads) void cluster_pool_kernel(
     }
     __syncthreads();
 
+    // Thread tid owns dim tid in the column passes: its word of a packed row
+    // and the selector of its half.
+    const int my_word = tid >> 1;
+    const uint32_t my_sel = bf16_select(tid);
     // Per-dim mean over valid queries in row order (csrc/ibcs.cu:130-140).
     {
         float sum = 0.0f;
@@ -183,11 +197,11 @@ __global__ __launch_bounds__(kClusterThreads) void cluster_pool_kernel(
         for (; i + 8 <= valid; i += 8) {  // 8 reads in flight, adds in row order
             float v[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] = block_elem(block, i + e, tid);
+            for (int e = 0; e < 8; ++e) v[e] = block_elem_sel(block, i + e, my_word, my_sel);
 #pragma unroll
             for (int e = 0; e < 8; ++e) sum += v[e];
         }
-        for (; i < valid; ++i) sum += block_elem(block, i, tid);
+        for (; i < valid; ++i) sum += block_elem_sel(block, i, my_word, my_sel);
         center_row[tid] = __fdiv_rn(sum, static_cast<float>(valid));
     }
     float x[kHeadDim];
@@ -206,7 +220,7 @@ __global__ __launch_bounds__(kClusterThreads) void cluster_pool_kernel(
     min_d = INFINITY;
     int assign = 0;
     for (int slot = 0; slot < kCentroids; ++slot) {
-        center_row[tid] = block_elem(block, center, tid);
+        center_row[tid] = block_elem_sel(block, center, my_word, my_sel);
         __syncthreads();
         if (live) {
             const float dist = lane_distance(x, center_row);
@@ -258,7 +272,7 @@ __global__ __launch_bounds__(kClusterThreads) void cluster_pool_kernel(
                     }
                     float v[8];
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) v[e] = block_elem(block, max(idx[e], 0), tid);
+                    for (int e = 0; e < 8; ++e) v[e] = block_elem_sel(block, max(idx[e], 0), my_word, my_sel);
 #pragma unroll
                     for (int e = 0; e < 8; ++e) sum += idx[e] >= 0 ? v[e] : 0.0f;
                 }
@@ -315,6 +329,8 @@ int64_t lse_stride(int64_t fb) { return (fb + 63) / 64 * 64; }
 
 int launch_cluster_pool(const void* q, const void* k, int64_t bh, int64_t n, void* centroids,
                         float* pops, void* pooled, float qk_scale_log2, const int32_t* order, hipStream_t stream) {
+    // The kernel addresses a head with 32-bit offsets.
+    if (n <= 0 || n > kMaxKvBlocks * kKvBlock) return set_error(1, "ibcs: %lld tokens per head", (long long)n);
     const int64_t qb = (n + kQueryBlock - 1) / kQueryBlock;
     dim3 grid(static_cast<unsigned>(qb), static_cast<unsigned>(bh));
     hipLaunchKernelGGL(cluster_pool_kernel, grid, dim3(kClusterThreads), 0, stream,
