@@ -28,6 +28,12 @@ Reported (one JSON line on stdout):
   cpu_baseline   the CPU oracle on all host threads (OpenMP) over one whole
                  head of the same workload, scaled by the head count.
 
+--static-plan prints a different line instead: the plan through
+ab_ibcs_sip_static (its workspace in the static array of
+libab_attention_static.so, heads in chunks that fit it) against ab_ibcs_sip
+with a caller workspace, median of --steps calls each, and whether the two
+plans are the same bits.
+
 --power prints a different line instead: socket power and graphics clock
 (median over `amd-smi metric -p -c` readings, taken from a child process
 every 0.2 s) while each part of the call runs back to back for
@@ -183,6 +189,52 @@ def power_legs(legs, seconds: float):
     return out
 
 
+def static_plan_timing(q, k, rows: int, samples: int, steps: int, workload: str) -> dict:
+    """Median ms of the plan through ab_ibcs_sip_static and through
+    ab_ibcs_sip with a caller workspace (same inputs and uniforms)."""
+    import torch
+
+    from ab_attention import _lib
+
+    lib, static = _lib.load(), _lib.load_static()
+    bh, n = q.shape[0] * q.shape[1], q.shape[2]
+    offsets = torch.rand(rows, device=q.device, generator=torch.Generator(q.device).manual_seed(42))
+    out = {}
+    plans = {}
+    ws_bytes = lib.ab_ibcs_sip_workspace_bytes(bh, n)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    st = _lib.stream(q.device)
+    for name in ("workspace", "static"):
+        ids = torch.empty(rows, samples, dtype=torch.int32, device=q.device)
+        w = torch.empty(rows, samples, dtype=torch.float32, device=q.device)
+        if name == "static":
+            call = lambda: static.ab_ibcs_sip_static(_lib.ptr(q), _lib.ptr(k), None, bh, n, _lib.ptr(offsets),  # noqa: E731
+                                                     samples, _lib.ptr(ids), _lib.ptr(w), st)
+        else:
+            call = lambda: lib.ab_ibcs_sip(_lib.ptr(q), _lib.ptr(k), None, bh, n, _lib.ptr(offsets), samples,  # noqa: E731
+                                           _lib.ptr(ws), ws_bytes, _lib.ptr(ids), _lib.ptr(w), st)
+        _lib.check(call())
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(max(steps, 1)):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            _lib.check(call())
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1))
+        out[name + "_ms"] = round(statistics.median(times), 3)
+        plans[name] = (ids, w)
+    same = (torch.equal(plans["static"][0], plans["workspace"][0])
+            and torch.equal(plans["static"][1].view(torch.int32), plans["workspace"][1].view(torch.int32)))
+    head_bytes = lib.ab_ibcs_sip_workspace_bytes(1, n)
+    chunk = min(bh, (512 << 20) // head_bytes) if head_bytes else 0
+    while chunk > 1 and lib.ab_ibcs_sip_workspace_bytes(chunk, n) > (512 << 20):
+        chunk -= 1
+    return {"workload": workload, "static_plan": dict(out, bit_identical=same, heads_per_static_chunk=chunk,
+                                                      workspace_bytes=ws_bytes)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -201,6 +253,8 @@ def main() -> int:
     ap.add_argument("--power", action="store_true",
                     help="only report socket power and graphics clock per part of the call (amd-smi)")
     ap.add_argument("--power-seconds", type=float, default=10.0)
+    ap.add_argument("--static-plan", action="store_true",
+                    help="only time the no-allocation plan (ab_ibcs_sip_static) against ab_ibcs_sip")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: every GPU box here has one GPU, and the path shards by "
@@ -255,6 +309,10 @@ def main() -> int:
                     plan.log_weights.reshape(rows, samples), order)
 
     stream = torch.cuda.current_stream()
+
+    if args.static_plan:
+        print(json.dumps(static_plan_timing(q, k, rows, samples, args.steps, cfg.name)), flush=True)
+        return 0
 
     if args.power:
         from ab_attention.paged import _prefill
