@@ -1,7 +1,7 @@
 // SIP on gfx950: inclusion probabilities pi = min(1, tau * m_j) with
 // sum(pi) = S, certainty blocks first (ascending, weight 0), then Madow
-// systematic draws with log2(1/pi) weights. One 1,024-thread workgroup per
-// row, 256 of whose threads play the reference's CUB block.
+// systematic draws with log2(1/pi) weights. One workgroup of 1,024 (or 512)
+// threads per row, 256 of whose threads play the reference's CUB block.
 //
 // Bit-exact restatement of csrc/sip.cu:33-167. Every fp64 sum keeps the
 // reference's association, which the reference gets from CUB:
@@ -15,11 +15,12 @@
 // contracts it); every other product is rounded before its sum, which the
 // build enforces with -ffp-contract=off.
 //
-// Workgroups have 1024 threads (16 waves) per row. The 256 "logical threads"
-// that define CUB's association (threads 0..255) own the ordered folds and
-// the chunk chains; the association-free phases (staging, marking, the last
-// residual, the draws) use all 1024 threads, which keeps enough waves per
-// SIMD to hide LDS and fp64 latency.
+// Workgroups have 1024 threads (16 waves) per row; the fused kernel gives
+// rows small enough for two per CU 512-thread workgroups. The 256 "logical
+// threads" that define CUB's association (threads 0..255) own the ordered
+// folds and the chunk chains; the association-free phases (staging, marking,
+// the last residual, the draws) use all the workgroup's threads, which keeps
+// enough waves per SIMD to hide LDS and fp64 latency.
 //
 // Two storage schemes, same bits:
 //   - sip_lds_kernel (rows whose masses and fp64 prefixes fit in LDS):
@@ -758,8 +759,8 @@ __global__ __launch_bounds__(kSipWorkers) void sip_lds_kernel(
 //   chunk (coarse_draws).
 // Two 512-thread workgroups per CU with kept prefixes were tried at c2
 // (81.9 KB each): 4.89 ms against 4.14 ms for this layout.
-template <bool kCoarse>
-__global__ __launch_bounds__(kSipWorkers) void sip_fused_kernel(
+template <int kWorkers, bool kCoarse>
+__global__ __launch_bounds__(kWorkers) void sip_fused_kernel(
     const _Float16* __restrict__ lse, const float* __restrict__ pops, const float* __restrict__ lse_max,
     const float* __restrict__ lse_den, int64_t ld, const float* __restrict__ offsets, int32_t* __restrict__ ids,
     float* __restrict__ logw, int population, int samples, int64_t rows, int force_exact) {
@@ -777,17 +778,17 @@ __global__ __launch_bounds__(kSipWorkers) void sip_fused_kernel(
         RowMasses rm;
         rm.load(pops, lse_max, lse_den, row);
         const _Float16* src = lse + row * kCentroids * ld;
-        for (int g0 = t; g0 < groups; g0 += 2 * kSipWorkers) {
+        for (int g0 = t; g0 < groups; g0 += 2 * kWorkers) {
             f16x8 h[2][kCentroids];
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
-                const int g = min(g0 + u * kSipWorkers, groups - 1);
+                const int g = min(g0 + u * kWorkers, groups - 1);
 #pragma unroll
                 for (int c = 0; c < kCentroids; ++c) h[u][c] = *reinterpret_cast<const f16x8*>(src + c * ld + 8 * g);
             }
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
-                const int g = g0 + u * kSipWorkers;
+                const int g = g0 + u * kWorkers;
                 if (g < groups) {
                     // Whole groups of 8: the masses of a last partial group
                     // past the population land in values[]' 8 padding
@@ -809,7 +810,7 @@ __global__ __launch_bounds__(kSipWorkers) void sip_fused_kernel(
         LdsRow rv{values};
         double sum = 0.0, mx = 0.0;
         if (t < kSipThreads) strided_partials<true>(rv, pop, sum, mx);
-        sip_row<kSipWorkers, kCoarse>(rv, sum, mx, prefix, sh, offsets[row], ids + row * int64_t(samples),
+        sip_row<kWorkers, kCoarse>(rv, sum, mx, prefix, sh, offsets[row], ids + row * int64_t(samples),
                                       logw + row * int64_t(samples), pop, samples, [] {}, force_exact);
     }
 }
@@ -877,18 +878,18 @@ static_assert(sip_fused_coarse_offset(kMaxKvBlocks) + coarse_keep(kMaxKvBlocks) 
 
 namespace {
 
-template <bool kCoarse>
+template <int kWorkers, bool kCoarse>
 int launch_fused(const _Float16* lse, const float* pops, const float* lse_max, const float* lse_den, int64_t ld,
                  const float* offsets, int64_t rows, int pop, int samples, int32_t* ids, float* logw,
                  int force_exact, hipStream_t stream) {
     const size_t bytes = sip_fused_lds_bytes(pop, kCoarse);
-    const void* fn = reinterpret_cast<const void*>(sip_fused_kernel<kCoarse>);
+    const void* fn = reinterpret_cast<const void*>(sip_fused_kernel<kWorkers, kCoarse>);
     if (int rc = ensure_lds_limit(fn, static_cast<int>(bytes))) return rc;
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kSipWorkers, bytes) != hipSuccess || per_cu < 1)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kWorkers, bytes) != hipSuccess || per_cu < 1)
         per_cu = 1;
     const int64_t grid = std::min<int64_t>(rows, int64_t(device_cu_count()) * per_cu);
-    hipLaunchKernelGGL(sip_fused_kernel<kCoarse>, dim3(static_cast<unsigned>(grid)), dim3(kSipWorkers), bytes,
+    hipLaunchKernelGGL((sip_fused_kernel<kWorkers, kCoarse>), dim3(static_cast<unsigned>(grid)), dim3(kWorkers), bytes,
                        stream, lse, pops, lse_max, lse_den, ld, offsets, ids, logw, pop, samples, rows,
                        force_exact);
     return check_launch("sip_fused_kernel");
@@ -908,10 +909,18 @@ int launch_sip_fused(const void* lse, const float* pops, const float* lse_max, c
     if (rows == 0) return 0;
     const _Float16* h = static_cast<const _Float16*>(lse);
     const int pop = static_cast<int>(population), s = static_cast<int>(samples);
-    if (sip_fused_lds_bytes(population, false) + kSipStaticLds <= kLdsLimit)
-        return launch_fused<false>(h, pops, lse_max, lse_den, ld, offsets, rows, pop, s, ids, logw, force_exact,
-                                   stream);
-    return launch_fused<true>(h, pops, lse_max, lse_den, ld, offsets, rows, pop, s, ids, logw, force_exact, stream);
+    const size_t full = sip_fused_lds_bytes(population, false) + kSipStaticLds;
+    // Rows small enough for two per CU (c1's 8,190 blocks: 49 KB) take
+    // 512-thread workgroups: a CU then samples two rows at once, where one
+    // 1,024-thread workgroup (16 waves x 93 VGPRs) would hold it alone.
+    if (2 * full <= kLdsLimit)
+        return launch_fused<kSipWorkers / 2, false>(h, pops, lse_max, lse_den, ld, offsets, rows, pop, s, ids, logw,
+                                                    force_exact, stream);
+    if (full <= kLdsLimit)
+        return launch_fused<kSipWorkers, false>(h, pops, lse_max, lse_den, ld, offsets, rows, pop, s, ids, logw,
+                                                force_exact, stream);
+    return launch_fused<kSipWorkers, true>(h, pops, lse_max, lse_den, ld, offsets, rows, pop, s, ids, logw,
+                                           force_exact, stream);
 }
 
 int launch_sip(const float* scores, const float* offsets, int64_t rows, int64_t population, int64_t samples,
