@@ -172,6 +172,30 @@ def test_prefill_neg_inf_blocks(oracle_mod):
         assert np.abs(got_lse[lo:hi] - ref_lse[0, lo:hi]).max() <= LSE_ABS, r
 
 
+def test_prefill_logit_range(oracle_mod):
+    """Weights far above the first tile's maximum. The kernel keeps each
+    query's first-tile maximum as its reference while no logit exceeds it by
+    more than 64 (base 2), and otherwise runs the row again with a moving
+    reference. Rows: a later tile 50 above (kept), 90 above (run again), the
+    last tile 200 above (run again), the first tile 100 above the rest (kept;
+    every later term is 2^-100 of it), +12 per tile (run again once the ramp
+    passes 64); all match the oracle."""
+    rng = np.random.default_rng(77)
+    torch.manual_seed(9)
+    n, samples = 1024, 64
+    rows, fb = n // 128, n // 4
+    q, k, v = (torch.randn(1, 1, n, 128).to(torch.bfloat16) for _ in range(3))
+    ids = np.sort(rng.choice(fb, size=(rows, samples), replace=True), axis=1).astype(np.int32)
+    logw = (rng.random((rows, samples)) * 3).astype(np.float32)
+    logw[0, 24:32] += 50.0
+    logw[1, 24:32] += 90.0
+    logw[2, 56:64] += 200.0
+    logw[3, :8] += 100.0
+    logw[4] += 12.0 * (np.arange(samples) // 8)
+    print("prefill logit range n=1024", flush=True)
+    _check(q, k, v, ids, logw, oracle_mod)
+
+
 def test_prefill_launch_chunks(oracle_mod):
     """91 heads x 128 query blocks = 11,648 rows: the prefill runs as two
     launches of whole generations (64 row slots per XCD, 16 slots per head on

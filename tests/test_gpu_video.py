@@ -53,6 +53,26 @@ def test_exact_attention(oracle_mod, nq, nk):
     assert np.abs(_f32(lse).reshape(2, nq) - ref_l).max() <= LSE_ABS
 
 
+def test_exact_attention_wide_logits(oracle_mod):
+    """Queries of magnitude ~60: the logits of a row span hundreds (base 2),
+    so most rows' maxima lie far above their first tile's and the dense walk
+    runs them with a moving reference; rows and LSEs still match the oracle."""
+    torch.manual_seed(23)
+    nq, nk = 512, 1024
+    print(f"exact attention wide logits nq={nq} nk={nk}", flush=True)
+    q = (torch.randn(1, 2, nq, 128) * 60).to(torch.bfloat16)
+    k = torch.randn(1, 2, nk, 128).to(torch.bfloat16)
+    v = torch.randn(1, 2, nk, 128).to(torch.bfloat16)
+    out, lse = exact_attention(q.cuda(), k.cuda(), v.cuda(), return_lse=True)
+    torch.cuda.synchronize()
+    rows = 2 * -(-nq // 128)
+    ids, w = _dense_plan(rows, nk // 4)
+    ref_o, ref_l = oracle_mod.prefill(_f32(q).reshape(2, nq, 128), _f32(k).reshape(2, nk, 128),
+                                      _f32(v).reshape(2, nk, 128), ids, w)
+    _close(_f32(out).reshape(2, nq, 128), ref_o)
+    assert np.abs(_f32(lse).reshape(2, nq) - ref_l).max() <= LSE_ABS
+
+
 def test_merge_states(oracle_mod):
     torch.manual_seed(7)
     n = 200
