@@ -51,6 +51,9 @@
 //   V: per page 8 blocks of 4 keys x 16 dims (128 B); inside block m the row
 //      of key r sits at position r ^ ((m >> 1) & 3), so each 16-lane group of
 //      a transposing read fetches one whole 128-byte block.
+// Dense attention (every KV4 block at weight 0, no page list) runs on
+// dense_kernel: the same rings, pipeline and two passes on
+// v_mfma_f32_16x16x32_bf16 tiles (see there).
 #include <algorithm>
 #include <type_traits>
 
@@ -80,7 +83,12 @@ constexpr float kSlack = 8.0f;
 // p <= 2^64 keeps every product and sum far from the float range.
 constexpr float kFastRange = 64.0f;
 
+// The dense kernel's LDS: the two rings and the votes.
+constexpr int kDenseVoteOffset = 2 * kRing * kTileBytes;
+constexpr int kDenseLdsBytes = kDenseVoteOffset + 16;          // 64 KiB + 16 B
+
 static_assert(kLdsBytes * 2 <= 160 * 1024, "two workgroups per CU must fit in LDS");
+static_assert(kDenseLdsBytes * 2 <= 160 * 1024, "two dense workgroups per CU must fit in LDS");
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
@@ -116,27 +124,44 @@ __device__ __forceinline__ void wait_and_barrier() {
     asm volatile("s_barrier" ::: "memory");
 }
 
-// kDense: every KV4 block of K/V in order (tile u holds blocks 8u .. 8u+7)
-// at weight 0, blocks past the end at -inf; ids and logw are not read. This
-// is dense attention with no page list in memory.
-template <bool kDense>
-__global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-    const int32_t* __restrict__ ids, const float* __restrict__ logw, uint16_t* __restrict__ out,
-    float* __restrict__ lse, int64_t n, int64_t n_kv, int64_t qb, int64_t rows, int fb, int samples,
-    float scale_log2, const int32_t* __restrict__ order, int64_t slot_base) {
-    extern __shared__ __align__(16) unsigned char smem[];
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// v_max_f32 without the NaN quieting the compiler adds around fmaxf of values
+// it cannot prove canonical (logits are finite or -inf).
+__device__ __forceinline__ float vmax(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+#pragma clang diagnostic pop
 
-    // XCD-aware row order. The hardware deals workgroups round-robin over the
-    // 8 XCDs, so workgroup w runs on XCD w % 8. Slot w / 8 walks the heads in
-    // order: at any time all XCDs work on the same head (its K/V stay in the
-    // shared last-level cache), each on a contiguous eighth of its query
-    // blocks (neighbouring blocks share most sampled pages in the XCD's L2).
-    // Within an XCD, slots s and s + 32 of each full generation of 64 slots
-    // run on the same CU (two workgroups per CU), so they take adjacent
-    // query blocks: their sampled pages overlap and they sweep them in step,
-    // which turns part of the gathers into L1 hits. A launch covers the
-    // slots from slot_base (a multiple of 64) on, on every XCD.
+// Maxima of a (query 0) and b (query 1) over the four lanes i, 16 + i,
+// 32 + i, 48 + i that hold a query in dense_kernel: three swaps of 16-lane
+// rows (rows of the results: a01 b01 a23 b23, then a b a b, then all a / all b).
+__device__ __forceinline__ void max_over_rows(float& a, float& b) {
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    const float m = vmax(__uint_as_float(s[0]), __uint_as_float(s[1]));
+    const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    const float m2 = vmax(__uint_as_float(t[0]), __uint_as_float(t[1]));
+    const auto u = __builtin_amdgcn_permlane16_swap(__float_as_uint(m2), __float_as_uint(m2), false, false);
+    a = __uint_as_float(u[0]);
+    b = __uint_as_float(u[1]);
+}
+
+// XCD-aware row order of the prefill kernels. The hardware deals workgroups
+// round-robin over the 8 XCDs, so workgroup w runs on XCD w % 8. Slot w / 8
+// walks the heads in order: at any time all XCDs work on the same head (its
+// K/V stay in the shared last-level cache), each on a contiguous eighth of its
+// query blocks (neighbouring blocks share most sampled pages in the XCD's L2).
+// Within an XCD, slots s and s + 32 of each full generation of 64 slots run
+// on the same CU (two workgroups per CU), so they take adjacent query blocks:
+// their sampled pages overlap and they sweep them in step, which turns part of
+// the gathers into L1 hits. A launch covers the slots from slot_base (a
+// multiple of 64) on, on every XCD. False for a slot past the rows.
+struct RowSlot {
+    int64_t bh, blk, row;
+};
+__device__ __forceinline__ bool row_slot(int64_t slot_base, int64_t qb, int64_t rows, RowSlot& rs) {
     const int64_t hw = blockIdx.x;
     const int64_t xcd = hw & 7, slot0 = slot_base + (hw >> 3);
     const int64_t per_xcd = (qb + 7) / 8;
@@ -144,10 +169,24 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
     const int64_t slot = (generation + 1) * 64 <= per_xcd * (rows / qb)
                              ? generation * 64 + 2 * (s64 & 31) + (s64 >> 5)
                              : slot0;
-    const int64_t bh = slot / per_xcd;
-    const int64_t blk = xcd * per_xcd + slot % per_xcd;
-    if (bh >= rows / qb || blk >= qb) return;
-    const int64_t row = bh * qb + blk;
+    rs.bh = slot / per_xcd;
+    rs.blk = xcd * per_xcd + slot % per_xcd;
+    if (rs.bh >= rows / qb || rs.blk >= qb) return false;
+    rs.row = rs.bh * qb + rs.blk;
+    return true;
+}
+
+// The sparse prefill: the row's listed KV4 blocks, with their log weights.
+__global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const int32_t* __restrict__ ids, const float* __restrict__ logw, uint16_t* __restrict__ out,
+    float* __restrict__ lse, int64_t n, int64_t n_kv, int64_t qb, int64_t rows, int fb, int samples,
+    float scale_log2, const int32_t* __restrict__ order, int64_t slot_base) {
+    extern __shared__ __align__(16) unsigned char smem[];
+
+    RowSlot rs;
+    if (!row_slot(slot_base, qb, rows, rs)) return;
+    const int64_t bh = rs.bh, blk = rs.blk, row = rs.row;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -211,11 +250,6 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
     // last tile (their transfers only keep the per-step count uniform).
     auto load_ids = [&](int u) {
         const int uc = min(u, tiles - 1);
-        if (kDense) {
-            const int id = uc * kTilePages + 2 * wave;
-            const u32x2 c = {uint32_t(min(id, fb - 1)), uint32_t(min(id + 1, fb - 1))};
-            return c;
-        }
         const u32x2 raw = *reinterpret_cast<const u32x2*>(smem + kIdsOffset + ((uc / kBatchTiles) & 1) * kBatchBytes +
                                                           ((uc % kBatchTiles) * kTilePages + 2 * wave) * 4);
         const u32x2 c = {uint32_t(min(max(static_cast<int>(raw[0]), 0), fb - 1)),
@@ -232,11 +266,6 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
     // holds key 8*(r/4) + 4*half + r%4, i.e. page 2(r/4) + half.
     auto load_weights = [&](int u, float (&wv)[4]) {
         const int uc = min(u, tiles - 1);
-        if (kDense) {
-#pragma unroll
-            for (int g = 0; g < 4; ++g) wv[g] = uc * kTilePages + 2 * g + half < fb ? 0.f : -INFINITY;
-            return;
-        }
         const float* ws = reinterpret_cast<const float*>(smem + kWeightsOffset +
                                                          ((uc / kBatchTiles) & 1) * kBatchBytes) +
                           (uc % kBatchTiles) * kTilePages;
@@ -309,7 +338,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
                     u32x2& idk, u32x2& idv) {
         constexpr bool kSafe = decltype(safe)::value;
         wait_and_barrier<2 * kGroupOps>();
-        if (!kDense && wave == 0 && t % kBatchTiles == kBatchTiles / 2 && (t / kBatchTiles + 1) * kBatchTiles < tiles)
+        if (wave == 0 && t % kBatchTiles == kBatchTiles / 2 && (t / kBatchTiles + 1) * kBatchTiles < tiles)
             issue_batch(t / kBatchTiles + 1);
         if constexpr (kSafe) {
             const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
@@ -400,7 +429,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
         // are in; K(4) goes into K(0)'s stage only after every wave has read
         // it. The last eight transfers before step 0 are then K(3), V(1), V(2),
         // K(4), as step 0's wait expects.
-        if (!kDense && wave == 0) issue_batch(0);
+        if (wave == 0) issue_batch(0);
         wait_and_barrier<0>();
         {
 #pragma unroll
@@ -508,6 +537,375 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
     }
 }
 
+// Dense attention: every KV4 block of K/V in order (tile u holds blocks
+// 8u .. 8u+7) at weight 0, blocks past the end at -inf, with no page list in
+// memory. Every row of a head reads the same pages in the same order, so the
+// gathers come from L2 and the MFMAs bound it; it runs on
+// v_mfma_f32_16x16x32_bf16, which takes less energy per FLOP than the
+// 32x32x16 form (the sparse kernel, bound by its gathers, keeps that one).
+// Same rings, transfers, pipeline and two passes as prefill_kernel; the LDS
+// holds the two rings and the votes (no page ids or weights).
+//
+// MFMA mapping (lane l = 16g + i, i < 16, g < 4): wave w owns queries
+// 32w + 16j + i (j = 0, 1).
+//   S^T = K Q^T : A = 16 keys x 32 dims (lane: key i, dims 8g..+7 of the
+//                 k-step), B = 32 dims x 16 queries (lane: query i, the same
+//                 dims); the lane gets keys 4g..4g+3 of each 16-key half kt of
+//                 the tile for query i: one whole KV4 block, page 4kt + g.
+//   O^T += V^T P^T: A = 16 dims x 32 keys, B = 32 keys x 16 queries; the
+//                 MFMA k-index 8g + 4kt + r is key r of page 4kt + g on both
+//                 operands, so P goes from the S^T accumulators to the B
+//                 operand unmoved, and the A operand is two transposing reads
+//                 (pages g and 4 + g).
+// A query spans the four lanes i, 16 + i, 32 + i, 48 + i; its maximum and sum
+// are combined over them with permlane swaps. V's dim blocks are placed by
+// the page's parity (position m ^ (page & 1), through the transfer's source
+// addresses): the four 16-lane groups of a transposing read fetch the same
+// dim block of four different pages, which then fall in opposite halves of
+// the banks.
+__global__ __launch_bounds__(kPfThreads, 2) void dense_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    uint16_t* __restrict__ out, float* __restrict__ lse, int64_t n, int64_t n_kv, int64_t qb, int64_t rows, int fb,
+    int samples, float scale_log2, int64_t slot_base) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    RowSlot rs;
+    if (!row_slot(slot_base, qb, rows, rs)) return;
+    const int64_t bh = rs.bh, blk = rs.blk;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int li = lane & 15, lg = lane >> 4;
+    const int tiles = samples / kTilePages;
+    auto token_of = [&](int j) { return blk * kQueryBlock + wave * 32 + 16 * j + li; };
+
+    // Q as the B operand of S^T = K Q^T: query 16j + li, dims 32ks + 8lg .. +8.
+    bf16x8 bq[2][4];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int64_t token = token_of(j);
+        const uint16_t* qrow = q + (bh * n + min<int64_t>(token, n - 1)) * kHeadDim + 8 * lg;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            u32x4 val = {0u, 0u, 0u, 0u};
+            if (token < n) val = *reinterpret_cast<const u32x4*>(qrow + 32 * ks);
+            bq[j][ks] = __builtin_bit_cast(bf16x8, val);
+        }
+    }
+
+    const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)smem));
+    const uint16_t* kbase = k + bh * n_kv * kHeadDim;
+    const uint16_t* vbase = v + bh * n_kv * kHeadDim;
+
+    // Transfers of this wave: pages 2w + e (e = 0, 1) of a K tile and of a V
+    // tile. Source offsets inside a page (1 KiB = 4 keys x 256 B) for lane j:
+    //   K: key r = j/16 at LDS chunk position j%16 holds chunk pos ^ (key & 15);
+    //   V: 128-byte position P = j/8 holds dim block m = P ^ e, key (j/2)%4,
+    //      dims 16m + 8(j%2).
+    uint32_t k_src[2], v_src[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int r = lane >> 4, pos = lane & 15;
+        const int key = 4 * (2 * wave + e) + r;
+        k_src[e] = uint32_t(r * 16 + (pos ^ (key & 15))) * 16u;
+        const int P = lane >> 3, sl = (lane >> 1) & 3, h = lane & 1;
+        v_src[e] = uint32_t(sl * 256 + (2 * (P ^ e) + h) * 16);
+    }
+    // This wave's two pages of tile u, clamped into the head; tiles past the
+    // row's end read its last tile (their transfers only keep the per-step
+    // count uniform).
+    auto load_ids = [&](int u) {
+        const int id = min(u, tiles - 1) * kTilePages + 2 * wave;
+        const u32x2 c = {uint32_t(min(id, fb - 1)), uint32_t(min(id + 1, fb - 1))};
+        return c;
+    };
+    auto dma_k = [&](int u, uint32_t id, int e) {
+        dma16(kbase, id * kPageBytes + k_src[e], lds0 + kKRing + (u & (kRing - 1)) * kTileBytes + (2 * wave + e) * kPageBytes);
+    };
+    auto dma_v = [&](int u, uint32_t id, int e) {
+        dma16(vbase, id * kPageBytes + v_src[e], lds0 + kVRing + (u & (kRing - 1)) * kTileBytes + (2 * wave + e) * kPageBytes);
+    };
+    // The weights of this lane's keys in tile u: pages lg and 4 + lg, 0 inside
+    // K/V and -inf past its end.
+    auto load_weights = [&](int u, float (&wv)[2]) {
+        const int uc = min(u, tiles - 1);
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) wv[kt] = uc * kTilePages + 4 * kt + lg < fb ? 0.f : -INFINITY;
+    };
+
+    // Operand-read addresses of this lane, absolute in LDS, so every read is
+    // one register plus the instruction's constant offset (ring stage, key
+    // half, dim block). K (A of S^T): key 16kt + li, chunk 4ks + lg at
+    // position chunk ^ li. V (A of O^T, transposing read): page lg (+4), dim
+    // block dt at position dt ^ (lg & 1), key li/4, dims 4(li%4) .. +3, so
+    // lane li receives dim 16dt + li of the page's four keys.
+    uint32_t k_abs[4], v_abs[2];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) k_abs[ks] = lds0 + kKRing + li * 256 + 16 * ((4 * ks + lg) ^ li);
+    {
+        const int par = lg & 1, base = kVRing + lg * kPageBytes + 32 * (li >> 2) + 8 * (li & 3);
+        v_abs[0] = lds0 + base + par * 128;  // even dt: position dt + par
+        v_abs[1] = lds0 + base - par * 128;  // odd dt: position dt - par
+    }
+    auto read_k = [&](int u, int f) {  // f = 4kt + ks
+        return *reinterpret_cast<const lds_u32x4*>(
+            static_cast<uintptr_t>(k_abs[f & 3] + (u & (kRing - 1)) * kTileBytes + (f >> 2) * 4096));
+    };
+    auto read_v_half = [&](int u, int dt, int h) {
+        const uint32_t a = v_abs[dt & 1] + (u & (kRing - 1)) * kTileBytes + dt * 128 + h * 4 * kPageBytes;
+        return __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_i16x4*>(static_cast<uintptr_t>(a)));
+    };
+
+    // O^T accumulators: o[dt][j] holds dims 16dt + 4lg .. +3 of query 16j + li.
+    f32x4 o_acc[8][2];
+    // Reference, running sum and state of query j. thr[j] is -inf until the
+    // query's first finite logit, kSlack after.
+    float m_run[2], l_run[2], thr[2];
+
+    // Step t, as in prefill_kernel: phase A computes S(t+1) beside p = 2^y of
+    // S(t) (sc[2kt + j]: key half kt, query j), the reads of V(t) and this
+    // step's four transfers; phase B computes O += V(t)^T P(t)^T beside the
+    // logits of S(t+1) and the reads of K(t+2). Fast pass: mx[0] is the
+    // running maximum of every logit of the lane. Safe pass: mx[j] is the
+    // maximum of query j over this lane's keys of S(t), and the reference
+    // moves lazily (kSlack). Rings and transfer lead as in prefill_kernel.
+    auto step = [&](auto safe, int t, f32x4 (&sc)[4], f32x4 (&sn)[4], float (&mx)[2], u32x4 (&ka)[8],
+                    float (&wn)[2], u32x2& idk, u32x2& idv) {
+        constexpr bool kSafe = decltype(safe)::value;
+        wait_and_barrier<2 * kGroupOps>();
+        if constexpr (kSafe) {
+            max_over_rows(mx[0], mx[1]);
+            const bool grow0 = mx[0] > thr[0], grow1 = mx[1] > thr[1];
+            if (__any(grow0 || grow1)) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const bool grow = j ? grow1 : grow0;
+                    const bool was_started = thr[j] == kSlack;
+                    const float shift = grow ? mx[j] : 0.f;
+                    // l_run and O are still zero before the first move, so alpha
+                    // is left at 1 there (2^-mx could overflow for a very
+                    // negative mx).
+                    const float alpha = was_started ? fast_exp2(-shift) : 1.f;
+                    thr[j] = grow ? kSlack : thr[j];
+                    m_run[j] += shift;
+                    l_run[j] *= alpha;
+#pragma unroll
+                    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) o_acc[dt][j][r] *= alpha;
+#pragma unroll
+                    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) sc[2 * kt + j][r] -= shift;
+                }
+            }
+        }
+        uint32_t pw[2][4];
+        float psum[2], p_prev = 0.f;
+        bf16x8 va[8];
+        i16x4 v_lo = {0, 0, 0, 0};
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sn[c][r] = 0.f;
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int x = 0; x < 16; ++x) {
+            const int ks = x >> 2, kt = (x >> 1) & 1, j = x & 1;
+            sn[2 * kt + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka[4 * kt + ks]),
+                                                                     bq[j][ks], sn[2 * kt + j], 0, 0, 0);
+            // p of element x of S(t): sc[c][r], c = x/4 = 2kt' + j', r = x%4.
+            const int c = x >> 2, r = x & 3;
+            const float p = fast_exp2(sc[c][r]);
+            if (r == 0) psum[c & 1] = (c >> 1) == 0 ? p : psum[c & 1] + p;
+            else psum[c & 1] += p;
+            if (x & 1) pw[c & 1][2 * (c >> 1) + (r >> 1)] = pack_bf16(p_prev, p);
+            p_prev = p;
+            const i16x4 vh = read_v_half(t, x >> 1, x & 1);
+            if (x & 1) va[x >> 1] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(v_lo, vh, 0, 1, 2, 3, 4, 5, 6, 7));
+            else v_lo = vh;
+            if (x == 2) dma_k(t + 5, idk[0], 0);
+            if (x == 6) dma_k(t + 5, idk[1], 1);
+            if (x == 10) dma_v(t + 3, idv[0], 0);
+            if (x == 14) dma_v(t + 3, idv[1], 1);
+            if (x == 4) load_weights(t + 1, wn);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        l_run[0] += psum[0];
+        l_run[1] += psum[1];
+        float wm[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) wm[c] = wn[c >> 1] - m_run[c & 1];
+        if constexpr (kSafe) {
+            mx[0] = -INFINITY;
+            mx[1] = -INFINITY;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(0);
+#pragma unroll
+        for (int x = 0; x < 16; ++x) {
+            const int dt = x >> 1, j = x & 1;
+            const u32x4 bw = {pw[j][0], pw[j][1], pw[j][2], pw[j][3]};
+            o_acc[dt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt], __builtin_bit_cast(bf16x8, bw), o_acc[dt][j], 0, 0, 0);
+            if ((x & 1) == 0) ka[x >> 1] = read_k(t + 2, x >> 1);
+            if (x & 1) {
+                // Logits of elements x-1 and x of S(t+1): sn[c][r], c = x/4.
+                const int c = x >> 2, r = x & 3;
+                const float y0 = __builtin_fmaf(sn[c][r - 1], scale_log2, wm[c]);
+                const float y1 = __builtin_fmaf(sn[c][r], scale_log2, wm[c]);
+                sn[c][r - 1] = y0;
+                sn[c][r] = y1;
+                float& m = mx[kSafe ? (c & 1) : 0];
+                m = fmaxf(fmaxf(m, y0), y1);  // one v_max3_f32
+            }
+            if (x == 12) idk = load_ids(t + 6);
+            if (x == 14) idv = load_ids(t + 4);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // One pass over the row's tiles, as in prefill_kernel.
+    auto pass = [&](auto safe) -> bool {
+        constexpr bool kSafe = decltype(safe)::value;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) o_acc[dt][j][r] = 0.f;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            m_run[j] = 0.f;
+            l_run[j] = 0.f;
+            thr[j] = -INFINITY;
+        }
+        // Prologue: K(0..3) and V(0..2); S(0) and K(1) into registers once
+        // K(0) and K(1) are in; K(4) goes into K(0)'s stage only after every
+        // wave has read it. The last eight transfers before step 0 are then
+        // K(3), V(1), V(2), K(4), as step 0's wait expects.
+        wait_and_barrier<0>();
+        {
+#pragma unroll
+            for (int u = 0; u < 3; ++u) {
+                const u32x2 ik = load_ids(u);
+                dma_k(u, ik[0], 0);
+                dma_k(u, ik[1], 1);
+            }
+            const u32x2 iv0 = load_ids(0);
+            dma_v(0, iv0[0], 0);
+            dma_v(0, iv0[1], 1);
+            const u32x2 ik3 = load_ids(3);
+            dma_k(3, ik3[0], 0);
+            dma_k(3, ik3[1], 1);
+            const u32x2 iv1 = load_ids(1), iv2 = load_ids(2);
+            dma_v(1, iv1[0], 0);
+            dma_v(1, iv1[1], 1);
+            dma_v(2, iv2[0], 0);
+            dma_v(2, iv2[1], 1);
+        }
+        const u32x2 ik4 = load_ids(4);
+        u32x2 idk = load_ids(5), idv = load_ids(3);
+        wait_and_barrier<10>();  // K(0), K(1) in; 10 newer transfers may be in flight
+        f32x4 s0[4], s1[4];
+        u32x4 ka[8];
+        {
+#pragma unroll
+            for (int f = 0; f < 8; ++f) ka[f] = read_k(0, f);
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) s0[c][r] = 0.f;
+#pragma unroll
+            for (int x = 0; x < 16; ++x) {
+                const int ks = x >> 2, kt = (x >> 1) & 1, j = x & 1;
+                s0[2 * kt + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka[4 * kt + ks]),
+                                                                         bq[j][ks], s0[2 * kt + j], 0, 0, 0);
+            }
+#pragma unroll
+            for (int f = 0; f < 8; ++f) ka[f] = read_k(1, f);
+        }
+        wait_and_barrier<63>();  // every wave's reads of K(0) are done (no transfer wait)
+        dma_k(4, ik4[0], 0);
+        dma_k(4, ik4[1], 1);
+        // Logits of S(0) (against reference 0).
+        float w0[2], mx[2] = {-INFINITY, -INFINITY};
+        load_weights(0, w0);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                s0[c][r] = __builtin_fmaf(s0[c][r], scale_log2, w0[c >> 1]);
+                mx[c & 1] = fmaxf(mx[c & 1], s0[c][r]);
+            }
+        }
+        if constexpr (!kSafe) {
+            // Each query's reference is the maximum of its first tile, over its
+            // four lanes; a query without a finite logit there fails the pass.
+            max_over_rows(mx[0], mx[1]);
+            bool all_started = true;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const bool started = mx[j] > -INFINITY;
+                all_started = all_started && started;
+                m_run[j] = started ? mx[j] : 0.f;
+                thr[j] = started ? kSlack : -INFINITY;
+#pragma unroll
+                for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) s0[2 * kt + j][r] -= m_run[j];
+            }
+            mx[0] = all_started ? -INFINITY : INFINITY;
+        }
+        int t = 0;
+        for (; t + 3 < tiles; t += 4) {
+            step(safe, t, s0, s1, mx, ka, w0, idk, idv);
+            step(safe, t + 1, s1, s0, mx, ka, w0, idk, idv);
+            step(safe, t + 2, s0, s1, mx, ka, w0, idk, idv);
+            step(safe, t + 3, s1, s0, mx, ka, w0, idk, idv);
+        }
+        for (; t + 1 < tiles; t += 2) {
+            step(safe, t, s0, s1, mx, ka, w0, idk, idv);
+            step(safe, t + 1, s1, s0, mx, ka, w0, idk, idv);
+        }
+        if (t < tiles) step(safe, t, s0, s1, mx, ka, w0, idk, idv);
+        // No transfer may still be landing when the workgroup's LDS is
+        // released or the rings are refilled.
+        __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0)
+        if constexpr (kSafe) return false;
+        // Workgroup vote: every wave publishes its flag, then all read all.
+        const uint32_t bad = __any(mx[0] > kFastRange) ? 1u : 0u;
+        uint32_t* votes = reinterpret_cast<uint32_t*>(smem + kDenseVoteOffset);
+        if (lane == 0) votes[wave] = bad;
+        wait_and_barrier<0>();
+        const u32x4 all = *reinterpret_cast<const u32x4*>(votes);
+        return (all[0] | all[1] | all[2] | all[3]) != 0u;
+    };
+    if (pass(std::false_type{})) pass(std::true_type{});
+
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        // Sum over the query's four lanes, in the same order in each of them.
+        const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(l_run[j]), __float_as_uint(l_run[j]), false, false);
+        const float l16 = __uint_as_float(s16[0]) + __uint_as_float(s16[1]);
+        const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(l16), __float_as_uint(l16), false, false);
+        const float l_tot = __uint_as_float(s32[0]) + __uint_as_float(s32[1]);
+        const int64_t token = token_of(j);
+        if (token < n) {
+            // A query whose every block has weight -inf (none here while K/V
+            // is not empty) gets o = 0 and lse = -inf.
+            const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+            uint16_t* orow = out + (bh * n + token) * kHeadDim + 4 * lg;
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) {
+                const u32x2 pk = {pack_bf16(o_acc[dt][j][0] * inv, o_acc[dt][j][1] * inv),
+                                  pack_bf16(o_acc[dt][j][2] * inv, o_acc[dt][j][3] * inv)};
+                *reinterpret_cast<u32x2*>(orow + 16 * dt) = pk;
+            }
+            if (lse != nullptr && lg == 0) lse[bh * n + token] = thr[j] == kSlack ? m_run[j] + log2f(l_tot) : -INFINITY;
+        }
+    }
+}
+
 // Plan ids of a permuted token layout -> KV4 pages of the stored layout:
 // out[i] = map[clamp(ids[i])], 4 ids per thread.
 __global__ __launch_bounds__(256) void remap_ids_kernel(const int32_t* __restrict__ ids, int64_t count,
@@ -595,8 +993,9 @@ int launch_prefill(const void* q, const void* k, const void* v, bool dense, int6
     const float scale_log2 = static_cast<float>(1.4426950408889634 / 11.313708498984761);  // log2(e)/sqrt(128)
     const int64_t per_xcd = (qb + 7) / 8;
     if (rows == 0) return 0;
-    auto kernel = dense ? prefill_kernel<true> : prefill_kernel<false>;
-    if (int rc = ensure_lds_limit(reinterpret_cast<const void*>(kernel), kLdsBytes)) return rc;
+    const void* kernel = dense ? reinterpret_cast<const void*>(dense_kernel) : reinterpret_cast<const void*>(prefill_kernel);
+    const int lds_bytes = dense ? kDenseLdsBytes : kLdsBytes;
+    if (int rc = ensure_lds_limit(kernel, lds_bytes)) return rc;
     // The rows are launched in chunks of about kRowsPerLaunch, each a whole
     // number of generations (64 row slots per XCD; a generation is what the
     // chip holds at once, two workgroups per CU). The rows resident on an XCD
@@ -610,12 +1009,20 @@ int launch_prefill(const void* q, const void* k, const void* v, bool dense, int6
     const int64_t per_launch = prefill_launch_slots(bh, n);
     for (int64_t slot_base = 0; slot_base < slots; slot_base += per_launch) {
         const int64_t count = std::min(per_launch, slots - slot_base);
-        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(count * 8)), dim3(kPfThreads), kLdsBytes, stream,
-                           static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
-                           static_cast<const uint16_t*>(v), ids, logw, static_cast<uint16_t*>(out), lse, n, n_kv, qb,
-                           rows, static_cast<int>(n_kv / kKvBlock), static_cast<int>(samples), scale_log2, order,
-                           slot_base);
-        if (int rc = check_launch("prefill_kernel")) return rc;
+        const dim3 grid(static_cast<unsigned>(count * 8)), block(kPfThreads);
+        const int fb = static_cast<int>(n_kv / kKvBlock), s = static_cast<int>(samples);
+        if (dense) {
+            hipLaunchKernelGGL(dense_kernel, grid, block, lds_bytes, stream, static_cast<const uint16_t*>(q),
+                               static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
+                               static_cast<uint16_t*>(out), lse, n, n_kv, qb, rows, fb, s, scale_log2, slot_base);
+            if (int rc = check_launch("dense_kernel")) return rc;
+        } else {
+            hipLaunchKernelGGL(prefill_kernel, grid, block, lds_bytes, stream, static_cast<const uint16_t*>(q),
+                               static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), ids, logw,
+                               static_cast<uint16_t*>(out), lse, n, n_kv, qb, rows, fb, s, scale_log2, order,
+                               slot_base);
+            if (int rc = check_launch("prefill_kernel")) return rc;
+        }
     }
     return 0;
 }

@@ -418,7 +418,7 @@ def main() -> int:
         result["dense"] = {"ms": round(dms, 3), "work_tflop": round(f_dense / 1e12, 3),
                            "tflops": round(f_dense / (dms * 1e-3) / 1e12, 1),
                            "frac": round(f_dense / (dms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
-                           "kernel": "prefill_kernel<dense>"}
+                           "kernel": "dense_kernel"}
     if not args.no_cpu_baseline and args.heads is None:
         result["cpu_baseline"] = cpu_baseline(q, k, v, cfg, args.cpu_head)
     print(json.dumps(result), flush=True)

@@ -140,10 +140,12 @@ def test_hunyuan_partition(oracle_mod, step, pad):
 
 
 def test_dense_equals_listed_pages(oracle_mod):
-    """exact_attention walks the blocks with no page list (ab_dense_prefill);
-    the same kernel over an explicit list of every block at weight 0 (padded
-    to a multiple of 8 with -inf) gives the same bits, and a longer case is
-    within the bf16 bars of the oracle on its first and last rows."""
+    """exact_attention walks the blocks with no page list (ab_dense_prefill,
+    the 16x16x32 dense kernel); the sparse kernel over an explicit list of
+    every block at weight 0 (padded to a multiple of 8 with -inf) computes the
+    same attention with other MFMA tiles: the two agree within bf16 rounding
+    (max-abs 2e-3, LSE 1e-4) everywhere, and both are within the bf16 bars of
+    the oracle on the first and last rows of each head."""
     from ab_attention.paged import _prefill_kv
     from ab_attention.video import _dense_pages
 
@@ -158,18 +160,19 @@ def test_dense_equals_listed_pages(oracle_mod):
     ids, w = _dense_pages(rows, nk // 4, q.device)
     out_l, lse_l = _prefill_kv(q, k, v, ids, w, return_lse=True)
     torch.cuda.synchronize()
-    assert torch.equal(out, out_l)
-    assert torch.equal(lse, lse_l)
+    assert float((out.float() - out_l.float()).abs().max()) <= 2e-3
+    assert float((lse - lse_l).abs().max()) <= 1e-4
     keep = np.array([0, rows // 2 - 1, rows // 2, rows - 1])
     ids_o, w_o = _dense_plan(rows, nk // 4)
     ref_o, ref_l = oracle_mod.prefill(_f32(q).reshape(2, nq, 128), _f32(k).reshape(2, nk, 128),
                                       _f32(v).reshape(2, nk, 128), ids_o, w_o, rows=keep)
-    got, got_l = _f32(out).reshape(2, nq, 128), _f32(lse).reshape(2, nq)
-    for r in keep:
-        bh, blk = divmod(int(r), rows // 2)
-        lo, hi = blk * 128, min(nq, blk * 128 + 128)
-        _close(got[bh, lo:hi], ref_o[bh, lo:hi])
-        assert np.abs(got_l[bh, lo:hi] - ref_l[bh, lo:hi]).max() <= LSE_ABS
+    for o_t, l_t in ((out, lse), (out_l, lse_l)):
+        got, got_l = _f32(o_t).reshape(2, nq, 128), _f32(l_t).reshape(2, nq)
+        for r in keep:
+            bh, blk = divmod(int(r), rows // 2)
+            lo, hi = blk * 128, min(nq, blk * 128 + 128)
+            _close(got[bh, lo:hi], ref_o[bh, lo:hi])
+            assert np.abs(got_l[bh, lo:hi] - ref_l[bh, lo:hi]).max() <= LSE_ABS
 
 
 def test_video_attention_plan_schedule(oracle_mod):
