@@ -98,9 +98,9 @@ typedef __attribute__((address_space(3))) unsigned char lds_u8;
 // Transposing LDS read: within each 16-lane group, lane i receives element
 // i%4 of the 8 bytes read by lanes 4r + i/4, for r = 0..3 (so the group reads
 // a 4 x 16 tile of 16-bit values, row r from lanes 4r..4r+3, and each lane
-// gets one column).
-__device__ __forceinline__ i16x4 lds_read_tr16(const unsigned char* p) {
-    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+// gets one column). lds is an absolute LDS byte address.
+__device__ __forceinline__ i16x4 lds_read_tr16(uint32_t lds) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_i16x4*>(static_cast<uintptr_t>(lds)));
 }
 
 #pragma clang diagnostic push
@@ -302,9 +302,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(
     // dims 32dt + 16(g%2) + 4q .. +3, so lane i receives dim 32dt + 16(g%2) + i.
     auto read_v = [&](int u, int j) {
         const uint32_t a0 = v_abs[j & 3] + (u & (kRing - 1)) * kTileBytes + (j >> 2) * 4096;
-        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_i16x4*>(static_cast<uintptr_t>(a0)));
-        const i16x4 hi =
-            __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_i16x4*>(static_cast<uintptr_t>(a0 + 2048)));
+        const i16x4 lo = lds_read_tr16(a0), hi = lds_read_tr16(a0 + 2048);
         return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
     };
 
@@ -652,7 +650,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void dense_kernel(
     };
     auto read_v_half = [&](int u, int dt, int h) {
         const uint32_t a = v_abs[dt & 1] + (u & (kRing - 1)) * kTileBytes + dt * 128 + h * 4 * kPageBytes;
-        return __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_i16x4*>(static_cast<uintptr_t>(a)));
+        return lds_read_tr16(a);
     };
 
     // O^T accumulators: o[dt][j] holds dims 16dt + 4lg .. +3 of query 16j + li.
