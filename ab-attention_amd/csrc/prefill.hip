@@ -745,7 +745,9 @@ __global__ __launch_bounds__(kPfThreads, 2) void dense_kernel(
             const int dt = x >> 1, j = x & 1;
             const u32x4 bw = {pw[j][0], pw[j][1], pw[j][2], pw[j][3]};
             o_acc[dt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt], __builtin_bit_cast(bf16x8, bw), o_acc[dt][j], 0, 0, 0);
-            if ((x & 1) == 0) ka[x >> 1] = read_k(t + 2, x >> 1);
+            // The K reads for the next step go out in the first half, so they
+            // have landed by the next step's barrier (which waits for them).
+            if (x < 8) ka[x] = read_k(t + 2, x);
             if (x & 1) {
                 // Logits of elements x-1 and x of S(t+1): sn[c][r], c = x/4.
                 const int c = x >> 2, r = x & 3;
