@@ -6,8 +6,9 @@ arithmetic is ``ab_paged_prefill_kv`` in libab_attention_hip.so: a bf16 MFMA
 flash-attention kernel that reads each row's KV4 blocks straight from K and
 V by their per-head ids and adds the SIP weight of each block to its logits
 (the reference's ABSipAttention variant, flashinfer_backend.py:30-59).
-``_prefill_dense`` is the same kernel walking every KV4 block of K/V at
-weight 0, with no page list in memory (ab_dense_prefill).
+``_prefill_dense`` runs the library's dense attention kernel, which walks
+every KV4 block of K/V at weight 0 with no page list in memory
+(ab_dense_prefill; the same rings and pipeline on 16x16x32 MFMA tiles).
 
 The reference translates per-head ids into a global page table and caches it
 per descriptor (flashinfer_backend.py:62-74, :202-217); the kernel here
@@ -107,7 +108,7 @@ def _prefill_kv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ids: torch.Te
 
 def _prefill_dense(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, return_lse: bool = False):
     """Dense attention of q bf16 [B,H,Nq,128] over every key of k/v bf16
-    [B,H,Nk,128] (Nk % 4 == 0) on the prefill kernel (ab_dense_prefill); the
+    [B,H,Nk,128] (Nk % 4 == 0) on the dense kernel (ab_dense_prefill); the
     page list is implicit, so nothing of size rows x blocks is built. Shapes
     are checked by the callers."""
     batch, heads, tokens, _ = q.shape

@@ -162,8 +162,8 @@ def exact_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, return
     """Dense non-causal attention of q [B,H,Nq,128] over k/v [B,H,Nk,128]
     (bf16, Nk divisible by 4); returns o bf16 [B,H,Nq,128] (and the base-2
     lse f32 [B,H,Nq]). The reference's _exact (video.py:13-28) on this
-    library's prefill kernel walking every KV4 block of K/V at weight 0, with
-    no page list in memory (ab_dense_prefill)."""
+    library's dense kernel, which walks every KV4 block of K/V at weight 0
+    with no page list in memory (ab_dense_prefill)."""
     _check_qkv(q, k, v)
     return _prefill_dense(q, k, v, return_lse=return_lse)
 

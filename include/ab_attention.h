@@ -123,9 +123,10 @@ int ab_paged_prefill_kv(const void *q, const void *k, const void *v, int64_t bat
 
 /* Dense attention of q [batch_heads, q_tokens, 128] over every key of k, v
  * [batch_heads, kv_tokens, 128] (kv_tokens divisible by 4), with the base-2
- * lse if lse != NULL: ab_paged_prefill_kv with every KV4 block listed at
- * weight 0, without a page list in memory (the kernel walks the blocks in
- * order). Replaces the FA3 single prefill of _exact
+ * lse if lse != NULL: the attention ab_paged_prefill_kv computes with every
+ * KV4 block listed at weight 0 (within bf16 rounding of it: a kernel of its
+ * own, on 16x16x32 MFMA tiles), without a page list in memory (the kernel
+ * walks the blocks in order). Replaces the FA3 single prefill of _exact
  * (ab_attention/video.py:13-28), which runs steps 1-10 and layer 0 of a
  * video (README.md:132-133). */
 int ab_dense_prefill(const void *q, const void *k, const void *v, int64_t batch_heads, int64_t q_tokens,
