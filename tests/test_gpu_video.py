@@ -73,6 +73,39 @@ def test_exact_attention_wide_logits(oracle_mod):
     assert np.abs(_f32(lse).reshape(2, nq) - ref_l).max() <= LSE_ABS
 
 
+def test_dense_launch_chunks(oracle_mod):
+    """Dense attention of 91 heads x 128 query blocks = 11,648 rows runs as two
+    launches of whole generations (the first covering heads 0-47), like the
+    sparse prefill. Every row is written (the output starts as NaN), and rows
+    at both ends of each launch match the oracle over all 4,096 blocks at
+    weight 0."""
+    from ab_attention import _lib
+
+    torch.manual_seed(12)
+    heads, n = 91, 128 * 128
+    print(f"dense launch chunks heads={heads} n={n}", flush=True)
+    q, k, v = (torch.randn(1, heads, n, 128).to(torch.bfloat16) for _ in range(3))
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    out = torch.full_like(qd, float("nan"))
+    lse = torch.full((1, heads, n), float("nan"), device="cuda")
+    lib = _lib.load()
+    _lib.check(lib.ab_dense_prefill(_lib.ptr(qd), _lib.ptr(kd), _lib.ptr(vd), heads, n, n, _lib.ptr(out), _lib.ptr(lse),
+                                    _lib.stream(qd.device)))
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all()) and bool(torch.isfinite(lse).all())
+    rows = heads * 128
+    keep = np.array([0, 47 * 128 + 5, 48 * 128 - 1, 48 * 128, 48 * 128 + 77, rows - 1])
+    ids, w = _dense_plan(rows, n // 4)
+    ref_o, ref_l = oracle_mod.prefill(_f32(q).reshape(heads, n, 128), _f32(k).reshape(heads, n, 128),
+                                      _f32(v).reshape(heads, n, 128), ids, w, rows=keep)
+    got, got_l = _f32(out).reshape(heads, n, 128), _f32(lse).reshape(heads, n)
+    for r in keep:
+        h, b = divmod(int(r), 128)
+        sl = slice(b * 128, b * 128 + 128)
+        _close(got[h, sl], ref_o[h, sl])
+        assert np.abs(got_l[h, sl] - ref_l[h, sl]).max() <= LSE_ABS, r
+
+
 def test_merge_states(oracle_mod):
     torch.manual_seed(7)
     n = 200
