@@ -43,7 +43,9 @@
 // tile maximum exceeds it by more than 8. The fast loop carries no rescale
 // branch and no per-step exchange between lanes, which leaves more of each
 // step's issue slots to the MFMAs (5-6 % less time at the benchmark
-// configurations, bit-identical results).
+// configurations). Where no later tile maximum passes the first tile's by
+// more than 8, the lazy pass never moves its reference either, and the two
+// passes give the same bits.
 // LDS tiles are swizzled so that the operand reads are bank-conflict free. A
 // transfer instruction writes 1 KiB contiguously (lane j at +16j), so the
 // swizzle is realised by the choice of each lane's source address:
