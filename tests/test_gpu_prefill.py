@@ -120,6 +120,40 @@ def test_prefill_c1_head_subset(oracle_mod):
         assert np.abs(got_lse[lo:hi] - ref_lse[0, lo:hi]).max() <= LSE_ABS
 
 
+def test_prefill_largest_head(oracle_mod):
+    """The longest head a plan can cover (build_plan's limit): 131,072
+    tokens (32,768 KV4 blocks, 1,024 query blocks), 64 sample pages; every
+    row lists the head's first and last KV4 blocks (page offsets up to
+    32 MiB - 1 KiB into K and V). The oracle checks the first and last three
+    rows and two in the middle."""
+    rng = np.random.default_rng(33)
+    torch.manual_seed(8)
+    n, samples = 131072, 2048
+    print(f"prefill largest head n={n}", flush=True)
+    q, k, v = (torch.randn(1, 1, n, 128).to(torch.bfloat16) for _ in range(3))
+    rows, fb = n // 128, n // 4
+    ids = np.sort(rng.choice(fb, size=(rows, samples), replace=True), axis=1).astype(np.int32)
+    ids[:, 0], ids[:, -1] = 0, fb - 1
+    logw = (rng.random((rows, samples)) * 4).astype(np.float32)
+    desc = torch.from_numpy(ids.reshape(rows, samples // 32, 32)).cuda()
+    w = torch.from_numpy(logw.reshape(rows, samples // 32, 32)).cuda()
+    out, lse = paged_attention(q.cuda(), k.cuda(), v.cuda(), desc, w, return_lse=True)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy().reshape(n, 128)
+    got_lse = lse.cpu().numpy().reshape(n)
+    assert np.isfinite(got).all() and np.isfinite(got_lse).all()
+    f32 = lambda t: t.float().numpy().reshape(1, n, 128)
+    keep = np.r_[0:3, 511:513, rows - 3:rows]
+    ref_o, ref_lse = oracle_mod.prefill(f32(q), f32(k), f32(v), ids, logw, rows=keep)
+    for r in keep:
+        lo, hi = r * 128, r * 128 + 128
+        e = np.abs(got[lo:hi] - ref_o[0, lo:hi])
+        assert e.max() <= MAX_ABS, (r, e.max())
+        rel = np.linalg.norm(got[lo:hi] - ref_o[0, lo:hi]) / np.linalg.norm(ref_o[0, lo:hi])
+        assert rel <= REL_L2, (r, rel)
+        assert np.abs(got_lse[lo:hi] - ref_lse[0, lo:hi]).max() <= LSE_ABS
+
+
 def test_prefill_workgroup_generations(oracle_mod):
     """7 heads x 80 query blocks: each XCD runs 70 row slots, one full
     generation of 64 (where the two workgroups sharing a CU take adjacent

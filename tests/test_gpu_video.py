@@ -73,6 +73,29 @@ def test_exact_attention_wide_logits(oracle_mod):
     assert np.abs(_f32(lse).reshape(2, nq) - ref_l).max() <= LSE_ABS
 
 
+def test_exact_attention_largest_head(oracle_mod):
+    """Dense attention over the longest head a plan can cover (131,072
+    tokens: 32,768 KV4 blocks, 1,024 query blocks), one head; the first and
+    last rows against the oracle over every block at weight 0."""
+    torch.manual_seed(31)
+    n = 131072
+    print(f"exact attention largest head n={n}", flush=True)
+    q, k, v = (torch.randn(1, 1, n, 128).to(torch.bfloat16) for _ in range(3))
+    out, lse = exact_attention(q.cuda(), k.cuda(), v.cuda(), return_lse=True)
+    torch.cuda.synchronize()
+    got, got_l = _f32(out).reshape(n, 128), _f32(lse).reshape(n)
+    assert np.isfinite(got).all() and np.isfinite(got_l).all()
+    rows = n // 128
+    keep = np.array([0, rows - 1])
+    ids, w = _dense_plan(rows, n // 4)
+    ref_o, ref_l = oracle_mod.prefill(_f32(q).reshape(1, n, 128), _f32(k).reshape(1, n, 128),
+                                      _f32(v).reshape(1, n, 128), ids, w, rows=keep)
+    for r in keep:
+        sl = slice(int(r) * 128, int(r) * 128 + 128)
+        _close(got[sl], ref_o[0, sl])
+        assert np.abs(got_l[sl] - ref_l[0, sl]).max() <= LSE_ABS, r
+
+
 def test_dense_launch_chunks(oracle_mod):
     """Dense attention of 91 heads x 128 query blocks = 11,648 rows runs as two
     launches of whole generations (the first covering heads 0-47), like the
